@@ -1,0 +1,161 @@
+/*
+ * torque_hip.h -- C ABI of the MI355X (gfx950) packed rotated KV-cache decode path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t.
+ * The library allocates nothing and keeps no device state; the caller owns
+ * all buffers (slabs, centroids, signs, workspaces, outputs).  Kernels are
+ * launched asynchronously on `stream`.  Return value: TQ_OK (0) or a negative
+ * TQ_ERR_* code; tq_last_error() gives the message (thread-local).
+ *
+ * Layouts (row-major, contiguous):
+ *   packed code slab  uint32 [L, Hkv, capacity, W],  W = ceil(D * bits / 32)
+ *                     (reference docs/contracts/packed-kv-layout.md:5-24)
+ *   queries           [L, Hq, D]   (float32 or float16)
+ *   outputs           float32 [L, Hq, D]
+ *   query head qh reads KV head qh / (Hq / Hkv)  (reference cache_mlx.py:706-722)
+ *
+ * Citations below name the reference interface each entry point replaces
+ * (paths relative to src/torque_mlx/ of cbun/torque-mlx).
+ */
+#ifndef TORQUE_HIP_H
+#define TORQUE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TQ_ABI_VERSION 1
+
+enum {
+  TQ_OK = 0,
+  TQ_ERR_BAD_ARG = -1,     /* shape / pointer / range error (Python: ValueError) */
+  TQ_ERR_UNSUPPORTED = -2, /* bits or head_dim outside {2,3,4} x {64,128,256} (ValueError) */
+  TQ_ERR_LAUNCH = -3       /* HIP launch failure (Python: RuntimeError) */
+};
+
+enum { TQ_F32 = 0, TQ_F16 = 1 };
+
+/* tq_append / tq_quantize_dequantize flags (reference cache_mlx.py:52-54) */
+enum { TQ_ROTATE_KEYS = 1, TQ_ROTATE_VALUES = 2 };
+/* tq_decode / tq_decode_dense flags (reference cache_mlx.py:188-196, 225-232) */
+enum { TQ_ROTATE_QUERY = 1, TQ_INVERSE_OUTPUT = 2 };
+
+int tq_abi_version(void);
+const char* tq_last_error(void);
+
+/* Structured Hadamard rotation of `rows` vectors of length head_dim.
+ * inverse == 0: y = sL * (H (sR * x)) / sqrt(D)   (rotation.py:88-94, 113-123)
+ * inverse != 0: y = sR * (H (sL * x)) / sqrt(D)   (rotation.py:96-102, 126-136)
+ * Bit-identical to the reference's float32 numpy transform (rotation.py:19-32). */
+int tq_fwht(const void* x, int x_dtype, float* y, int64_t rows, int head_dim, const float* signs_left,
+            const float* signs_right, int inverse, hipStream_t stream);
+
+/* Quantize already-rotated float32 rows by boundary count and bit-pack them:
+ * values [rows, D] -> packed [rows, W].  Replaces quantize_and_pack_rows_metal
+ * (mlx_ops.py:256-292, 342-371); bit-exact to quantize + pack_indices_batched
+ * (quantization.py:139-148, 176-201). */
+int tq_quantize_pack(const float* values, int64_t rows, int head_dim, int bits, const float* boundaries,
+                     uint32_t* packed, hipStream_t stream);
+
+/* Fused rotate -> quantize -> bit-pack append of seq_new tokens for every
+ * layer and KV head, written in place at slab position `offset`.
+ * keys/values [L, Hkv, seq_new, D] (dtype TQ_F32 or TQ_F16).  Flags select
+ * which streams are rotated.  Replaces TorqueKVCacheMLX._append_packed_tokens
+ * and quantize_and_pack_rows_dual_metal (cache_mlx.py:396-418, 504-521;
+ * mlx_ops.py:295-339, 374-412). */
+int tq_append(const void* keys, const void* values, int dtype, int num_layers, int kv_heads, int64_t seq_new,
+              int head_dim, int bits, const float* signs_left, const float* signs_right, int flags,
+              const float* key_boundaries, const float* value_boundaries, uint32_t* key_codes,
+              uint32_t* value_codes, int64_t capacity, int64_t offset, hipStream_t stream);
+
+/* Rotate (per flags) -> quantize -> dequantize to dense float32 centroid values,
+ * rows [rows, D] -> out [rows, D]; values/value_out may be NULL.  Replaces
+ * TorqueKVCacheMLX._quantize_rows on the current token (cache_mlx.py:246-255, 496-502). */
+int tq_quantize_dequantize(const void* keys, const void* values, int dtype, int64_t rows, int head_dim, int bits,
+                           const float* signs_left, const float* signs_right, int flags,
+                           const float* key_boundaries, const float* value_boundaries,
+                           const float* key_centroids, const float* value_centroids, float* key_out,
+                           float* value_out, hipStream_t stream);
+
+/* Unpack + dequantize the first seq_len tokens of `groups` slab rows:
+ * codes [groups, capacity, W] -> out float32 [groups, seq_len, D].
+ * Replaces TorqueKVCache.export_dequantized (cache.py:189-214). */
+int tq_unpack_dequantize(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, int head_dim,
+                         int bits, const float* centroids, float* out, hipStream_t stream);
+
+/* Split count the decode kernels use when n_splits <= 0 is passed. */
+int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int head_dim, int64_t seq_len,
+                             int num_cus);
+
+/* Bytes of workspace tq_decode / tq_decode_dense need for n_splits splits
+ * (n_splits <= 0: enough for the default split count on any sequence length
+ * with num_cus compute units).  The workspace must be zero-filled once when it
+ * is allocated; the kernels leave its counters at zero on exit.  Calls that
+ * share one workspace must be ordered (same stream). */
+size_t tq_decode_workspace_bytes(int num_layers, int kv_heads, int query_heads, int head_dim, int n_splits,
+                                 int num_cus);
+
+/* Fused packed-code decode attention for one query token per query head:
+ * optional query rotation, split-K over the sequence with an online softmax
+ * in the rotated basis, cross-workgroup log-sum-exp merge and optional
+ * inverse rotation, all in one launch.  current_keys / current_values
+ * (float32 [L, Hkv, D], already rotated and dequantized, or NULL) join the
+ * softmax as one extra dense token.  Replaces decode_packed_attention_split_batched
+ * (mlx_ops.py:571-595), ..._with_current (mlx_ops.py:598-660),
+ * decode_packed_attention (mlx_ops.py:663-692) and the decode flow of
+ * TorqueKVCacheMLX.decode_mlx / decode_mlx_with_current (cache_mlx.py:173-302). */
+int tq_decode(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads, int head_dim,
+              int bits, const uint32_t* key_codes, const uint32_t* value_codes, int64_t capacity,
+              int64_t seq_len, const float* key_centroids, const float* value_centroids,
+              const float* signs_left, const float* signs_right, int flags, const float* current_keys,
+              const float* current_values, int n_splits, void* workspace, float* out, hipStream_t stream);
+
+/* Same as tq_decode; start/stop events (may be NULL) are bound to the kernel
+ * itself, so hipEventElapsedTime gives its execution time. */
+int tq_decode_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
+                    int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
+                    int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,
+                    const float* signs_left, const float* signs_right, int flags, const float* current_keys,
+                    const float* current_values, int n_splits, void* workspace, float* out, hipStream_t stream,
+                    hipEvent_t start, hipEvent_t stop);
+
+/* Dense-KV decode attention with the same split-K structure, for float16 or
+ * float32 K/V slabs [L, Hkv, capacity, D].  With kv_dtype TQ_F16 this is the
+ * fp16-dense comparator of the reference's qwen-decode benchmark (MLX-LM
+ * KVCache + scaled_dot_product_attention, qwen_benchmark.py:313-314, 395-402);
+ * with TQ_F32 and the rotation flags it is the fp32 rotated baseline of the
+ * synthetic benchmark (benchmarking.py:62-71). */
+int tq_decode_dense(const void* query, int query_dtype, const void* keys, const void* values, int kv_dtype,
+                    int num_layers, int query_heads, int kv_heads, int head_dim, int64_t capacity, int64_t seq_len,
+                    const float* signs_left, const float* signs_right, int flags, int n_splits, void* workspace,
+                    float* out, hipStream_t stream);
+
+int tq_decode_dense_timed(const void* query, int query_dtype, const void* keys, const void* values,
+                          int kv_dtype, int num_layers, int query_heads, int kv_heads, int head_dim,
+                          int64_t capacity, int64_t seq_len, const float* signs_left, const float* signs_right,
+                          int flags, int n_splits, void* workspace, float* out, hipStream_t stream,
+                          hipEvent_t start, hipEvent_t stop);
+
+/* Raw (unscaled) packed scores: query [B, D] (rotated), codes [B, S, W] -> scores [B, S].
+ * Replaces score_packed_query_batched (mlx_ops.py:113-145, 501-531). */
+int tq_score_packed(const float* query, const uint32_t* codes, int batch, int64_t seq_len, int head_dim, int bits,
+                    const float* centroids, float* scores, hipStream_t stream);
+
+/* Row softmax of scale * scores: [B, S] -> [B, S] (the mx.softmax of mlx_ops.py:588). */
+int tq_softmax_rows(const float* scores, int batch, int64_t seq_len, float scale, float* weights,
+                    hipStream_t stream);
+
+/* Weighted packed value sum: weights [B, S], codes [B, S, W] -> out [B, D].
+ * Replaces accumulate_packed_values_batched (mlx_ops.py:148-178, 534-568). */
+int tq_accumulate_packed(const float* weights, const uint32_t* codes, int batch, int64_t seq_len, int head_dim,
+                         int bits, const float* centroids, float* out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TORQUE_HIP_H */

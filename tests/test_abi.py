@@ -1,0 +1,82 @@
+"""The C-ABI library loads and exports every entry point include/torque_hip.h declares.
+
+CPU only: nothing here launches a kernel (the calls below return before any
+device work -- argument errors and pure host queries).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "torque_hip.h"
+
+
+def _declared() -> dict[str, int]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(tq_[a-z_]+)\s*\(([^;{]*?)\)\s*;", text):
+        args = m.group(2).strip()
+        decls[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return decls
+
+
+def test_header_declares_the_path():
+    decls = _declared()
+    for name in ("tq_fwht", "tq_quantize_pack", "tq_append", "tq_decode", "tq_decode_dense", "tq_last_error"):
+        assert name in decls
+
+
+def test_library_exports_every_declared_symbol():
+    from torque_hip import _lib
+
+    lib = ctypes.CDLL(str(_lib.library_path()))
+    for name, nargs in _declared().items():
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes binding"
+        assert len(_lib.SIGNATURES[name][1]) == nargs, f"{name}: binding has {len(_lib.SIGNATURES[name][1])} args, header {nargs}"
+
+
+def test_host_only_entry_points():
+    from torque_hip import _lib
+
+    lib = _lib.load()
+    assert lib.tq_abi_version() == 1
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 32768, 256) == 64
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 7, 256) == 1
+    assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, 64, 256) > 64 * 8 * 4 * 128 * 4
+    assert lib.tq_decode_workspace_bytes(1, 8, 30, 128, 64, 256) == 0  # Hq not divisible
+
+
+@pytest.mark.parametrize(
+    ("args", "code", "message"),
+    [
+        (dict(head_dim=96), -2, "Unsupported head dimension: 96"),
+        (dict(bits=5), -2, "Unsupported bit width: 5"),
+        (dict(query_heads=30), -1, "must be divisible by kv_heads"),
+        (dict(capacity=5), -1, "capacity must be >= seq_len"),
+    ],
+)
+def test_decode_argument_errors(args, code, message):
+    from torque_hip import _lib
+
+    lib = _lib.load()
+    p = dict(head_dim=128, bits=4, query_heads=32, capacity=10)
+    p.update(args)
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    rc = lib.tq_decode(fake, 0, 1, p["query_heads"], 8, p["head_dim"], p["bits"], fake, fake, p["capacity"], 10,
+                       fake, fake, None, None, 0, None, None, 0, fake, fake, None)
+    assert rc == code
+    assert message in lib.tq_last_error().decode()
+
+
+def test_status_mapping():
+    from torque_hip import _lib
+
+    _lib.load()
+    with pytest.raises(ValueError, match="Unsupported bit width"):
+        _lib.call("tq_quantize_pack", 0x1000, 4, 64, 7, 0x1000, 0x1000, None)

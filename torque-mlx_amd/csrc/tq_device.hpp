@@ -1,0 +1,276 @@
+// Device-side building blocks for the packed rotated KV-cache kernels (gfx950).
+//
+// Wavefront = 64 lanes.  A D-vector held by one wavefront is split so that
+// lane l owns elements [l*E, l*E + E), E = D / 64.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tq {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // 4 wavefronts per workgroup
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v);
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) {
+  return v;
+}
+template <>
+__device__ __forceinline__ float to_f32<__half>(__half v) {
+  return __half2float(v);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------
+// Walsh-Hadamard transform of one D-vector held by a wavefront.
+//
+// Butterfly order and operands are those of the reference's float32 numpy
+// transform (rotation.py:19-32): steps 1, 2, 4, ..., each producing
+// (left + right, left - right) with `left` the lower index.  Every element
+// sees the same sequence of IEEE float32 adds/subtracts with the same
+// operands, so the result is bit-identical to the reference.
+template <int D>
+__device__ __forceinline__ void wave_fwht(float (&v)[D / kWave]) {
+  constexpr int E = D / kWave;
+  const int lane = lane_id();
+#pragma unroll
+  for (int s = 1; s < E; s <<= 1) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      if ((i & s) == 0) {
+        const float a = v[i], b = v[i + s];
+        v[i] = __fadd_rn(a, b);
+        v[i + s] = __fsub_rn(a, b);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    const bool upper = (lane & m) != 0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const float other = __shfl_xor(v[i], m);
+      v[i] = upper ? __fsub_rn(other, v[i]) : __fadd_rn(v[i], other);
+    }
+  }
+}
+
+// y = s_second * (H (s_first * x)) / sqrt(D), with the reference's operation
+// order (rotation.py:88-102): multiply by the first signs, transform, divide
+// by float32(sqrt(D)) (correctly rounded), multiply by the second signs.
+// apply():   s_first = signs_right, s_second = signs_left
+// inverse(): s_first = signs_left,  s_second = signs_right
+template <int D>
+__device__ __forceinline__ void wave_rotate(float (&v)[D / kWave], const float* __restrict__ s_first,
+                                            const float* __restrict__ s_second, float sqrt_d) {
+  constexpr int E = D / kWave;
+  const int base = lane_id() * E;
+#pragma unroll
+  for (int i = 0; i < E; ++i) v[i] = __fmul_rn(v[i], s_first[base + i]);
+  wave_fwht<D>(v);
+#pragma unroll
+  for (int i = 0; i < E; ++i) v[i] = __fmul_rn(__fdiv_rn(v[i], sqrt_d), s_second[base + i]);
+}
+
+// ---------------------------------------------------------------------------
+// Quantizer: code = number of boundaries strictly below x (quantization.py:139-148,
+// mlx_ops.py:271-273).  Ties go to the lower code; NaN gives 0.
+template <int BITS>
+__device__ __forceinline__ uint32_t quantize_count(float x, const float* __restrict__ bnd) {
+  uint32_t c = 0;
+#pragma unroll
+  for (int k = 0; k < (1 << BITS) - 1; ++k) c += (x > bnd[k]) ? 1u : 0u;
+  return c;
+}
+
+// Packed word `w` of a row whose codes sit in `codes[0..D)`: LSB-first
+// bitstream, code j at bit j*BITS, the high bits of a code that crosses a word
+// boundary continue at bit 0 of the next word (quantization.py:156-173).
+template <int BITS, int D>
+__device__ __forceinline__ uint32_t pack_word(const uint8_t* codes, int w) {
+  const int bit0 = 32 * w;
+  const int j0 = bit0 / BITS;
+  int j1 = (bit0 + 31) / BITS;
+  if (j1 > D - 1) j1 = D - 1;
+  uint32_t word = 0;
+  for (int j = j0; j <= j1; ++j) {
+    const int o = j * BITS - bit0;
+    const uint32_t c = codes[j];
+    word |= (o >= 0) ? (c << o) : (c >> (-o));
+  }
+  return word;
+}
+
+// Code j of a packed row (straddle-aware), for the unpack kernels.
+template <int BITS>
+__device__ __forceinline__ uint32_t unpack_code(const uint32_t* __restrict__ row, int j) {
+  const int bit = j * BITS;
+  const int w = bit >> 5, s = bit & 31;
+  uint32_t v = row[w] >> s;
+  if (s + BITS > 32) v |= row[w + 1] << (32 - s);
+  return v & ((1u << BITS) - 1u);
+}
+
+// ---------------------------------------------------------------------------
+// Lane-slice formats for the decode kernels.  A token row is split into
+// D / kSliceDims slices; one lane owns one slice of one token.  `load` reads
+// the slice's raw bits from the row, `decode` turns them into kSliceDims
+// float32 values using an LDS lookup table built from the centroids.
+
+// 4-bit: 16 dims = 8 bytes = words 2s, 2s+1; one table entry per byte holds
+// the centroids of its low and high nibble.
+struct PackedB4 {
+  static constexpr int kBits = 4;
+  static constexpr int kSliceDims = 16;
+  static constexpr bool kHasLut = true;
+  static constexpr int kLutEntries = 256;
+  using LutT = float2;
+  struct Raw {
+    uint32_t a, b;
+  };
+  template <int D>
+  static constexpr int row_bytes() {
+    return D * kBits / 8;
+  }
+  __device__ static LutT lut_entry(int e, const float* __restrict__ c) { return make_float2(c[e & 15], c[e >> 4]); }
+  __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
+    const uint2 v = *reinterpret_cast<const uint2*>(row + 8 * slice);
+    return {v.x, v.y};
+  }
+  __device__ static void decode(const Raw& r, int /*slice*/, const LutT* __restrict__ lut, float (&x)[kSliceDims]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t word = (j < 4) ? r.a : r.b;
+      const uint32_t byte = (word >> (8 * (j & 3))) & 0xffu;
+      const float2 c = lut[byte];
+      x[2 * j] = c.x;
+      x[2 * j + 1] = c.y;
+    }
+  }
+};
+
+// 2-bit: 16 dims = 1 word; one table entry per byte holds 4 centroids.
+struct PackedB2 {
+  static constexpr int kBits = 2;
+  static constexpr int kSliceDims = 16;
+  static constexpr bool kHasLut = true;
+  static constexpr int kLutEntries = 256;
+  using LutT = float4;
+  struct Raw {
+    uint32_t a;
+  };
+  template <int D>
+  static constexpr int row_bytes() {
+    return D * kBits / 8;
+  }
+  __device__ static LutT lut_entry(int e, const float* __restrict__ c) {
+    return make_float4(c[e & 3], c[(e >> 2) & 3], c[(e >> 4) & 3], c[(e >> 6) & 3]);
+  }
+  __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
+    return {*reinterpret_cast<const uint32_t*>(row + 4 * slice)};
+  }
+  __device__ static void decode(const Raw& r, int /*slice*/, const LutT* __restrict__ lut, float (&x)[kSliceDims]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 c = lut[(r.a >> (8 * j)) & 0xffu];
+      x[4 * j] = c.x;
+      x[4 * j + 1] = c.y;
+      x[4 * j + 2] = c.z;
+      x[4 * j + 3] = c.w;
+    }
+  }
+};
+
+// 3-bit: 16 dims = 48 bits starting at bit 48*s, i.e. words (3s)>>1 and the
+// next one, shifted right by 16 for odd slices.  Codes straddle word
+// boundaries; one table entry per 6-bit code pair holds both centroids.
+struct PackedB3 {
+  static constexpr int kBits = 3;
+  static constexpr int kSliceDims = 16;
+  static constexpr bool kHasLut = true;
+  static constexpr int kLutEntries = 64;
+  using LutT = float2;
+  struct Raw {
+    uint32_t a, b;
+  };
+  template <int D>
+  static constexpr int row_bytes() {
+    return D * kBits / 8;
+  }
+  __device__ static LutT lut_entry(int e, const float* __restrict__ c) { return make_float2(c[e & 7], c[e >> 3]); }
+  __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + ((3 * slice) >> 1);
+    return {w[0], w[1]};
+  }
+  __device__ static void decode(const Raw& r, int slice, const LutT* __restrict__ lut, float (&x)[kSliceDims]) {
+    const uint64_t z = ((static_cast<uint64_t>(r.b) << 32) | r.a) >> ((slice & 1) * 16);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float2 c = lut[static_cast<uint32_t>(z >> (6 * j)) & 63u];
+      x[2 * j] = c.x;
+      x[2 * j + 1] = c.y;
+    }
+  }
+};
+
+// Dense float16 rows: 8 dims = 16 bytes per slice.
+struct DenseF16 {
+  static constexpr int kSliceDims = 8;
+  static constexpr bool kHasLut = false;
+  static constexpr int kLutEntries = 1;
+  using LutT = float;
+  struct Raw {
+    uint4 v;
+  };
+  template <int D>
+  static constexpr int row_bytes() {
+    return D * 2;
+  }
+  __device__ static LutT lut_entry(int, const float*) { return 0.f; }
+  __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
+    return {*reinterpret_cast<const uint4*>(row + 16 * slice)};
+  }
+  __device__ static void decode(const Raw& r, int, const LutT*, float (&x)[kSliceDims]) {
+    const uint32_t w[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[2 * j] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[j] & 0xffffu)));
+      x[2 * j + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[j] >> 16)));
+    }
+  }
+};
+
+// Dense float32 rows: 4 dims = 16 bytes per slice.
+struct DenseF32 {
+  static constexpr int kSliceDims = 4;
+  static constexpr bool kHasLut = false;
+  static constexpr int kLutEntries = 1;
+  using LutT = float;
+  struct Raw {
+    float4 v;
+  };
+  template <int D>
+  static constexpr int row_bytes() {
+    return D * 4;
+  }
+  __device__ static LutT lut_entry(int, const float*) { return 0.f; }
+  __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
+    return {*reinterpret_cast<const float4*>(row + 16 * slice)};
+  }
+  __device__ static void decode(const Raw& r, int, const LutT*, float (&x)[kSliceDims]) {
+    x[0] = r.v.x;
+    x[1] = r.v.y;
+    x[2] = r.v.z;
+    x[3] = r.v.w;
+  }
+};
+
+}  // namespace tq
