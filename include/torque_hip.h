@@ -93,16 +93,17 @@ int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int 
 
 /* Bytes of workspace tq_decode / tq_decode_dense need for n_splits splits
  * (n_splits <= 0: enough for the default split count on any sequence length
- * with num_cus compute units).  The workspace must be zero-filled once when it
- * is allocated; the kernels leave its counters at zero on exit.  Calls that
- * share one workspace must be ordered (same stream). */
+ * with num_cus compute units).  The workspace holds per-split partial results
+ * between the two launches of one call; it needs no initialisation.  Calls
+ * that share one workspace must be ordered (same stream). */
 size_t tq_decode_workspace_bytes(int num_layers, int kv_heads, int query_heads, int head_dim, int n_splits,
                                  int num_cus);
 
 /* Fused packed-code decode attention for one query token per query head:
  * optional query rotation, split-K over the sequence with an online softmax
- * in the rotated basis, cross-workgroup log-sum-exp merge and optional
- * inverse rotation, all in one launch.  current_keys / current_values
+ * in the rotated basis, log-sum-exp merge of the splits and optional inverse
+ * rotation.  One launch when the sequence is not split (n_splits resolves to
+ * 1), otherwise the split kernel followed by a small merge kernel.  current_keys / current_values
  * (float32 [L, Hkv, D], already rotated and dequantized, or NULL) join the
  * softmax as one extra dense token.  Replaces decode_packed_attention_split_batched
  * (mlx_ops.py:571-595), ..._with_current (mlx_ops.py:598-660),
@@ -114,8 +115,9 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
               const float* signs_left, const float* signs_right, int flags, const float* current_keys,
               const float* current_values, int n_splits, void* workspace, float* out, hipStream_t stream);
 
-/* Same as tq_decode; start/stop events (may be NULL) are bound to the kernel
- * itself, so hipEventElapsedTime gives its execution time. */
+/* Same as tq_decode; start/stop events (may be NULL) are bound to the split
+ * kernel itself, so hipEventElapsedTime gives its execution time (the merge
+ * kernel, when launched, follows it on the stream). */
 int tq_decode_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
                     int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
                     int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,

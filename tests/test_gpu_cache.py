@@ -359,3 +359,27 @@ def test_shape_forms_and_errors(hip_device):
     assert tuple(mask.shape) == (3, 4) and bool(mask[0, 0]) and not bool(mask[0, 2])
     two.reset()
     assert two.sequence_length == 0 and not two._store.key_codes.any().item()
+
+
+def test_split_merge_handoff_is_coherent(hip_device):
+    """Many-split decodes hand partials between workgroups through one shared
+    workspace; alternate two caches so a stale partial from the previous call
+    would show up.  Single-split decodes need no hand-off and are the check."""
+    import torque_hip as th
+
+    rng = np.random.default_rng(77)
+    caches, queries = [], []
+    for seed, s in ((0, 20000), (1, 9000)):
+        cfg = th.TorqueConfig(bit_width=4, head_dim=128, num_layers=1, kv_heads=8, rotation_seed=seed)
+        c = th.TorqueKVCacheHIP(config=cfg, initial_capacity=s)
+        c.append_many(key=rng.normal(size=(1, 8, s, 128)).astype(np.float16),
+                      value=rng.normal(size=(1, 8, s, 128)).astype(np.float16))
+        caches.append(c)
+        queries.append(torch.from_numpy(rng.normal(size=(1, 32, 128)).astype(np.float32)).to(hip_device))
+    refs = [c._store.decode(q, rotate_query=True, inverse_output=True, n_splits=1).cpu().numpy()
+            for c, q in zip(caches, queries)]
+    for rep in range(40):
+        i = rep % 2
+        ns = (16, 64, 256, 37)[rep % 4]
+        got = caches[i]._store.decode(queries[i], rotate_query=True, inverse_output=True, n_splits=ns).cpu().numpy()
+        np.testing.assert_allclose(got, refs[i], atol=2e-6, rtol=1e-5, err_msg=f"rep {rep} cache {i} n_splits {ns}")

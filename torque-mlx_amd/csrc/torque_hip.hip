@@ -67,6 +67,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;
 constexpr int kMaxSplits = 256;
 constexpr int kTokensPerIter = 2;  // tokens per lane group per loop iteration
+constexpr int kPrefetchIters = 2;  // loop iterations whose loads are in flight ahead
 
 // ============================================================== rotation
 
@@ -178,40 +179,67 @@ struct DecodeArgs {
   const float* cur_v;
   int n_splits;
   int64_t split_len;
-  unsigned* counters;  // [units]
-  float2* ws_ml;       // [units, n_splits, HG]  (max, sum) per split
-  float* ws_acc;       // [units, n_splits, HG, D]
-  float* out;          // [L, Hq, D]
+  float* ws_ml;   // [L * Hq, n_splits, 2]  (max, sum) of each split, log2 units
+  float* ws_acc;  // [L * Hq, n_splits, D]  value accumulator of each split
+  float* ws_q;    // [L * Hq, D]            scaled rotated queries
+  float* out;     // [L, Hq, D]
 };
+
+// Finish one output row held by a wavefront: optional extra dense token
+// (decode-with-current), normalisation, optional inverse rotation, store.
+// A[D]: accumulator relative to max M (log2 units), L: softmax sum.
+template <int D>
+__device__ __forceinline__ void finish_row(const float* A, float M, float L, const float* qs, const float* ck,
+                                           const float* cv, int inverse, const float* signs_left,
+                                           const float* signs_right, float sqrt_d, float* dst) {
+  constexpr int E = D / kWave;
+  const int lane = lane_id();
+  float e[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) e[i] = A[lane * E + i];
+  if (ck != nullptr) {
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) dot = fmaf(qs[lane * E + i], ck[lane * E + i], dot);
+    dot = group_sum<kWave>(dot);
+    const float mn = fmaxf(M, dot);
+    const float f_old = L > 0.f ? fast_exp2(M - mn) : 0.f;
+    const float f_cur = fast_exp2(dot - mn);
+#pragma unroll
+    for (int i = 0; i < E; ++i) e[i] = e[i] * f_old + cv[lane * E + i] * f_cur;
+    L = L * f_old + f_cur;
+  }
+#pragma unroll
+  for (int i = 0; i < E; ++i) e[i] = L > 0.f ? e[i] / L : 0.f;
+  if (inverse) wave_rotate<D>(e, signs_left, signs_right, sqrt_d);
+#pragma unroll
+  for (int i = 0; i < E; ++i) dst[lane * E + i] = e[i];
+}
 
 template <class Fmt, int D, int HG>
 __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   constexpr int SD = Fmt::kSliceDims;
   constexpr int LPT = D / SD;        // lanes per token
-  constexpr int TPW = kWave / LPT;   // tokens per wavefront step
+  constexpr int TPW = kWave / LPT;   // tokens (lane groups) per wavefront
   constexpr int TPB = kWavesPerBlock * TPW;
   constexpr int U = kTokensPerIter;
   constexpr int E = D / kWave;
   constexpr int ROW = Fmt::template row_bytes<D>();
+  constexpr int NV = HG * SD;        // accumulator values per lane
   using Raw = typename Fmt::Raw;
 
   __shared__ typename Fmt::LutT s_lut[2][Fmt::kLutEntries];
   __shared__ float s_q[HG][D];
-  __shared__ float s_acc[HG][D];
-  __shared__ float s_l[HG];
+  __shared__ float s_red[kWavesPerBlock][HG * D];
   __shared__ float s_mw[kWavesPerBlock][HG];
-  __shared__ float s_f[kMaxSplits][HG];
-  __shared__ float s_M[HG];
-  __shared__ float s_L[HG];
-  __shared__ float s_cur[HG];
-  __shared__ int s_last;
+  __shared__ float s_lw[kWavesPerBlock][HG];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
   const int gi = lane / LPT, slice = lane % LPT;
 
   // ---- work item.  Consecutive workgroup ids land on different XCDs
-  // (round robin over 8); remap so the splits of one head group share an XCD
-  // and their partials stay in that XCD's L2 for the merge.
+  // (round robin over 8); remap so the splits of one head group are
+  // dispatched to the same XCD and share its L2.
   const int units = a.num_layers * a.kv_heads * a.n_hgroups;
   const int64_t nblk = static_cast<int64_t>(units) * a.n_splits;
   int64_t g = blockIdx.x;
@@ -223,18 +251,16 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   const int layer = lkv / a.kv_heads, kvh = lkv - layer * a.kv_heads;
   const int qh0 = kvh * a.group + hg * HG;
 
-  // ---- tables, accumulators
+  // ---- centroid tables
   if constexpr (Fmt::kHasLut) {
     for (int e = tid; e < Fmt::kLutEntries; e += kBlock) {
       s_lut[0][e] = Fmt::lut_entry(e, a.cent_k);
       s_lut[1][e] = Fmt::lut_entry(e, a.cent_v);
     }
   }
-  for (int o = tid; o < HG * D; o += kBlock) (&s_acc[0][0])[o] = 0.f;
-  if (tid < HG) s_l[tid] = 0.f;
 
   // ---- queries: optional rotation (bit-identical to the reference), then
-  // fold the softmax scale and log2(e) in.
+  // the softmax scale and log2(e) folded in, so scores are in log2 units.
   if (wave < HG) {
     float e[E];
     const int64_t qoff = (static_cast<int64_t>(layer) * a.query_heads + qh0 + wave) * D + lane * E;
@@ -268,8 +294,10 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     for (int i = 0; i < SD; ++i) acc[h][i] = 0.f;
   }
 
-  // ---- main loop: wavefront `wave`, lane group `gi` takes tokens
-  // t0 + wave*TPW + gi + k*TPB; one wavefront load covers TPW consecutive rows.
+  // ---- main loop.  Wavefront `wave`, lane group `gi` takes tokens
+  // t0 + wave*TPW + gi + k*TPB: one wavefront load covers TPW consecutive
+  // rows.  Each iteration handles U tokens per lane group: U x HG partial
+  // scores, one group reduction (DPP), one softmax update, U value updates.
   const int64_t t0 = static_cast<int64_t>(split) * a.split_len;
   const int64_t t1 = min(a.seq_len, t0 + a.split_len);
   const uint8_t* kbase = a.k + static_cast<int64_t>(lkv) * a.cap * ROW;
@@ -292,172 +320,271 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     }
   };
 
-  auto process = [&](const Raw& kr, const Raw& vr, bool valid) {
-    float x[SD];
-    Fmt::decode(kr, slice, lut_k, x);
-    float s[HG];
+  auto process = [&](const Raw (&kr)[U], const Raw (&vr)[U], int64_t base) {
+    float s[U][HG];
 #pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      float acc_s = 0.f;
+    for (int u = 0; u < U; ++u) {
+      float x[SD];
+      Fmt::decode(kr[u], slice, lut_k, x);
 #pragma unroll
-      for (int i = 0; i < SD; ++i) acc_s = fmaf(qv[h][i], x[i], acc_s);
-      s[h] = acc_s;
+      for (int h = 0; h < HG; ++h) {
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < SD; i += 2) {
+          d0 = fmaf(qv[h][i], x[i], d0);
+          d1 = fmaf(qv[h][i + 1], x[i + 1], d1);
+        }
+        s[u][h] = d0 + d1;
+      }
     }
 #pragma unroll
-    for (int mask = 1; mask < LPT; mask <<= 1)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int h = 0; h < HG; ++h) s[h] += __shfl_xor(s[h], mask);
-    float p[HG];
+      for (int h = 0; h < HG; ++h) s[u][h] = group_sum<LPT>(s[u][h]);
+    bool valid[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) valid[u] = base + u * TPB + gi < t1;
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
-      const float sv = valid ? s[h] : -INFINITY;
-      if (sv > m[h] + kRescaleThreshold) {
-        const float alpha = fast_exp2(m[h] - sv);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u) mx = valid[u] ? fmaxf(mx, s[u][h]) : mx;
+      if (mx > m[h] + kRescaleThreshold) {
+        const float alpha = fast_exp2(m[h] - mx);
         lsum[h] *= alpha;
 #pragma unroll
         for (int i = 0; i < SD; ++i) acc[h][i] *= alpha;
-        m[h] = sv;
+        m[h] = mx;
       }
-      p[h] = valid ? fast_exp2(sv - m[h]) : 0.f;
-      lsum[h] += p[h];
     }
-    Fmt::decode(vr, slice, lut_v, x);
+    float p[U][HG];
 #pragma unroll
-    for (int h = 0; h < HG; ++h)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int i = 0; i < SD; ++i) acc[h][i] = fmaf(p[h], x[i], acc[h][i]);
+      for (int h = 0; h < HG; ++h) {
+        p[u][h] = valid[u] ? fast_exp2(s[u][h] - m[h]) : 0.f;
+        lsum[h] += p[u][h];
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float x[SD];
+      Fmt::decode(vr[u], slice, lut_v, x);
+#pragma unroll
+      for (int h = 0; h < HG; ++h)
+#pragma unroll
+        for (int i = 0; i < SD; ++i) acc[h][i] = fmaf(p[u][h], x[i], acc[h][i]);
+    }
   };
 
   {
+    // Software pipeline over a ring of NB = PF + 1 iteration slots: the loads
+    // of iteration i + PF are issued before iteration i is processed.
+    constexpr int PF = kPrefetchIters;
+    constexpr int NB = PF + 1;
     const int64_t first = t0 + wave * TPW;
-    Raw kc[U], vc[U];
-    load_iter(first, kc, vc);
-    for (int64_t base = first; base < t1; base += U * TPB) {  // uniform per wavefront
-      Raw kn[U], vn[U];
-      load_iter(base + U * TPB, kn, vn);
+    const int64_t stride = static_cast<int64_t>(U) * TPB;
+    const int64_t n_iter = first < t1 ? (t1 - first + stride - 1) / stride : 0;  // uniform per wavefront
+    Raw kr[NB][U], vr[NB][U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) process(kc[u], vc[u], base + u * TPB + gi < t1);
+    for (int j = 0; j < PF; ++j) load_iter(first + j * stride, kr[j], vr[j]);
+    for (int64_t it = 0; it < n_iter; it += NB) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        kc[u] = kn[u];
-        vc[u] = vn[u];
+      for (int j = 0; j < NB; ++j) {
+        if (it + j >= n_iter) break;
+        const int64_t base = first + (it + j) * stride;
+        load_iter(base + PF * stride, kr[(j + PF) % NB], vr[(j + PF) % NB]);
+        process(kr[j], vr[j], base);
       }
     }
   }
 
-  // ---- combine the lane groups of this workgroup (log-sum-exp)
-  float mw[HG];
+  // ---- combine the lane groups of this workgroup (log-sum-exp).
+  // Workgroup max per head, then every lane rescales to it.
+  float M[HG];
 #pragma unroll
   for (int h = 0; h < HG; ++h) {
-    mw[h] = m[h];
+    float mw = m[h];
 #pragma unroll
-    for (int mask = LPT; mask < kWave; mask <<= 1) mw[h] = fmaxf(mw[h], __shfl_xor(mw[h], mask));
+    for (int mask = LPT; mask < kWave; mask <<= 1) mw = fmaxf(mw, __shfl_xor(mw, mask));
+    if (lane == 0) s_mw[wave][h] = mw;
   }
-  if (lane == 0)
-#pragma unroll
-    for (int h = 0; h < HG; ++h) s_mw[wave][h] = mw[h];
   __syncthreads();
-  float M[HG];
 #pragma unroll
   for (int h = 0; h < HG; ++h) {
     M[h] = s_mw[0][h];
 #pragma unroll
     for (int w = 1; w < kWavesPerBlock; ++w) M[h] = fmaxf(M[h], s_mw[w][h]);
+  }
+  float buf[NV];
+#pragma unroll
+  for (int h = 0; h < HG; ++h) {
     const float f = lsum[h] > 0.f ? fast_exp2(m[h] - M[h]) : 0.f;
+    float lw = lsum[h] * f;
 #pragma unroll
-    for (int i = 0; i < SD; ++i) atomicAdd(&s_acc[h][slice * SD + i], acc[h][i] * f);
-    if (slice == 0) atomicAdd(&s_l[h], lsum[h] * f);
+    for (int mask = LPT; mask < kWave; mask <<= 1) lw += __shfl_xor(lw, mask);
+    if (lane == 0) s_lw[wave][h] = lw;
+#pragma unroll
+    for (int i = 0; i < SD; ++i) buf[h * SD + i] = acc[h][i] * f;
   }
-  __syncthreads();
-
-  const int64_t pidx = static_cast<int64_t>(unit) * a.n_splits + split;
-  float* pacc = a.ws_acc + pidx * (HG * D);
-  for (int o = tid; o < HG * D; o += kBlock) pacc[o] = (&s_acc[0][0])[o];
-  if (tid < HG) a.ws_ml[pidx * HG + tid] = make_float2(M[tid], s_l[tid]);
-
-  // ---- last workgroup of this head group merges all splits
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = atomicAdd(&a.counters[unit], 1u);
-    s_last = (prev == static_cast<unsigned>(a.n_splits - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  const int ns = a.n_splits;
-  const float2* ml = a.ws_ml + static_cast<int64_t>(unit) * ns * HG;
-  const float* accs = a.ws_acc + static_cast<int64_t>(unit) * ns * (HG * D);
-  if (wave < HG) {
-    const int h = wave;
-    constexpr int PER = kMaxSplits / kWave;
-    float2 v[PER];
-    float mx = -INFINITY;
+  // Reduce-scatter the accumulators over the TPW lane groups of the
+  // wavefront: afterwards lane (gi, slice) holds values
+  // [gi * NV / TPW, (gi + 1) * NV / TPW) of its slice, summed over groups.
+  {
+    int len = NV;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int s = lane + k * kWave;
-      v[k] = s < ns ? ml[s * HG + h] : make_float2(-INFINITY, 0.f);
-      mx = fmaxf(mx, v[k].x);
+    for (int gm = TPW / 2; gm >= 1; gm >>= 1) {
+      const int lm = gm * LPT;
+      const bool upper = (lane & lm) != 0;
+      len >>= 1;
+#pragma unroll
+      for (int k = 0; k < NV / 2; ++k) {
+        if (k < len) {
+          const float send = upper ? buf[k] : buf[k + len];
+          const float keep = upper ? buf[k + len] : buf[k];
+          buf[k] = keep + __shfl_xor(send, lm);
+        }
+      }
     }
+    constexpr int W = NV / TPW;
 #pragma unroll
-    for (int mask = 1; mask < kWave; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask));
-    float lt = 0.f;
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int s = lane + k * kWave;
-      const float f = v[k].y > 0.f ? fast_exp2(v[k].x - mx) : 0.f;
-      if (s < ns) s_f[s][h] = f;
-      lt += v[k].y * f;
-    }
-#pragma unroll
-    for (int mask = 1; mask < kWave; mask <<= 1) lt += __shfl_xor(lt, mask);
-    float sc = -INFINITY;
-    if (a.cur_k != nullptr) {
-      const float* ck = a.cur_k + static_cast<int64_t>(lkv) * D + lane * E;
-      float dot = 0.f;
-#pragma unroll
-      for (int i = 0; i < E; ++i) dot = fmaf(s_q[h][lane * E + i], ck[i], dot);
-#pragma unroll
-      for (int mask = 1; mask < kWave; mask <<= 1) dot += __shfl_xor(dot, mask);
-      sc = dot;
-    }
-    if (lane == 0) {
-      s_M[h] = mx;
-      s_L[h] = lt;
-      s_cur[h] = sc;
+    for (int k = 0; k < W; ++k) {
+      const int v = gi * W + k;
+      const int h = v / SD, i = v - h * SD;
+      s_red[wave][h * D + slice * SD + i] = buf[k];
     }
   }
   __syncthreads();
 
+  // ---- one split: this workgroup holds the whole result and finishes it.
+  const int64_t qhg0 = static_cast<int64_t>(layer) * a.query_heads + qh0;
+  if (a.n_splits == 1) {
+    for (int o = tid; o < HG * D; o += kBlock) {
+      float v = s_red[0][o];
+#pragma unroll
+      for (int w = 1; w < kWavesPerBlock; ++w) v += s_red[w][o];
+      s_red[0][o] = v;
+    }
+    __syncthreads();
+    if (wave < HG) {
+      float l = s_lw[0][wave];
+#pragma unroll
+      for (int w = 1; w < kWavesPerBlock; ++w) l += s_lw[w][wave];
+      const bool cur = a.cur_k != nullptr;
+      finish_row<D>(&s_red[0][wave * D], M[wave], l, s_q[wave], cur ? a.cur_k + static_cast<int64_t>(lkv) * D : nullptr,
+                    cur ? a.cur_v + static_cast<int64_t>(lkv) * D : nullptr, a.inverse_output, a.signs_left,
+                    a.signs_right, a.sqrt_d, a.out + (qhg0 + wave) * D);
+    }
+    return;
+  }
+
+  // ---- several splits: publish this split's partial for merge_kernel.
   for (int o = tid; o < HG * D; o += kBlock) {
+    float v = s_red[0][o];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) v += s_red[w][o];
     const int h = o / D, d = o - h * D;
-    float A = 0.f;
-#pragma unroll 16
-    for (int s = 0; s < ns; ++s) A = fmaf(accs[static_cast<int64_t>(s) * (HG * D) + o], s_f[s][h], A);
-    float L = s_L[h];
-    if (a.cur_k != nullptr) {
-      const float Mm = s_M[h], sc = s_cur[h];
-      const float Mn = fmaxf(Mm, sc);
-      const float f_old = L > 0.f ? fast_exp2(Mm - Mn) : 0.f;
-      const float f_cur = fast_exp2(sc - Mn);
-      A = A * f_old + a.cur_v[static_cast<int64_t>(lkv) * D + d] * f_cur;
-      L = L * f_old + f_cur;
-    }
-    s_acc[h][d] = L > 0.f ? A / L : 0.f;
+    a.ws_acc[((qhg0 + h) * a.n_splits + split) * D + d] = v;
   }
-  __syncthreads();
+  if (tid < HG) {
+    float l = s_lw[0][tid];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) l += s_lw[w][tid];
+    a.ws_ml[((qhg0 + tid) * a.n_splits + split) * 2] = M[tid];
+    a.ws_ml[((qhg0 + tid) * a.n_splits + split) * 2 + 1] = l;
+  }
+  if (split == 0)
+    for (int o = tid; o < HG * D; o += kBlock) a.ws_q[qhg0 * D + o] = (&s_q[0][0])[o];
+}
 
-  if (wave < HG) {
-    float e[E];
+// Log-sum-exp merge of the splits of one query head (one workgroup per head):
+// M = max_s M_s, L = sum_s L_s 2^(M_s - M), A = sum_s A_s 2^(M_s - M), then
+// the optional current token, normalisation and inverse rotation.
+struct MergeArgs {
+  int query_heads, kv_heads, group, n_splits;
+  const float* ws_ml;
+  const float* ws_acc;
+  const float* ws_q;
+  const float* cur_k;
+  const float* cur_v;
+  const float* signs_left;
+  const float* signs_right;
+  float sqrt_d;
+  int inverse_output;
+  float* out;
+};
+
+template <int D>
+__global__ __launch_bounds__(kBlock) void merge_kernel(const MergeArgs a) {
+  constexpr int E = D / kWave;
+  constexpr int kChunk = 16;  // splits per wavefront per round of loads
+  __shared__ float s_f[kMaxSplits];
+  __shared__ float s_red[kWavesPerBlock];
+  __shared__ float s_part[kWavesPerBlock][D];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
+  const int64_t qhg = blockIdx.x;
+  const int layer = static_cast<int>(qhg / a.query_heads);
+  const int qh = static_cast<int>(qhg - static_cast<int64_t>(layer) * a.query_heads);
+  const int64_t lkv = static_cast<int64_t>(layer) * a.kv_heads + qh / a.group;
+  const int ns = a.n_splits;
+  const float* ml = a.ws_ml + qhg * ns * 2;
+  const float* acc = a.ws_acc + qhg * ns * D;
+
+  // Wavefront w takes splits w, w + 4, ...; its first chunk of accumulator
+  // loads is issued before the (max, sum) reduction.
+  float vals[kChunk][E];
+  auto load_chunk = [&](int c) {
 #pragma unroll
-    for (int i = 0; i < E; ++i) e[i] = s_acc[wave][lane * E + i];
-    if (a.inverse_output) wave_rotate<D>(e, a.signs_left, a.signs_right, a.sqrt_d);
-    float* dst = a.out + (static_cast<int64_t>(layer) * a.query_heads + qh0 + wave) * D + lane * E;
+    for (int k = 0; k < kChunk; ++k) {
+      const int s = (c * kChunk + k) * kWavesPerBlock + wave;
 #pragma unroll
-    for (int i = 0; i < E; ++i) dst[i] = e[i];
+      for (int i = 0; i < E; ++i) vals[k][i] = s < ns ? acc[static_cast<int64_t>(s) * D + lane * E + i] : 0.f;
+    }
+  };
+  load_chunk(0);
+  const float ms = tid < ns ? ml[tid * 2] : -INFINITY;
+  const float ls = tid < ns ? ml[tid * 2 + 1] : 0.f;
+  float mx = ms;
+#pragma unroll
+  for (int mask = 1; mask < kWave; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask));
+  if (lane == 0) s_red[wave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float f = ls > 0.f ? fast_exp2(ms - M) : 0.f;
+  if (tid < ns) s_f[tid] = f;
+  const float lw = group_sum<kWave>(ls * f);
+  __syncthreads();
+  if (lane == 0) s_red[wave] = lw;
+  __syncthreads();
+  const float L = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+
+  float part[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) part[i] = 0.f;
+  const int chunks = (ns + kChunk * kWavesPerBlock - 1) / (kChunk * kWavesPerBlock);
+  for (int c = 0; c < chunks; ++c) {
+    if (c > 0) load_chunk(c);
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      const int s = (c * kChunk + k) * kWavesPerBlock + wave;
+      const float fs = s < ns ? s_f[s] : 0.f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) part[i] = fmaf(vals[k][i], fs, part[i]);
+    }
   }
-  if (tid == 0) a.counters[unit] = 0u;  // ready for the next call
+#pragma unroll
+  for (int i = 0; i < E; ++i) s_part[wave][lane * E + i] = part[i];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int d = lane * E + i;
+      s_part[0][d] = s_part[0][d] + s_part[1][d] + s_part[2][d] + s_part[3][d];
+    }
+    const bool cur = a.cur_k != nullptr;
+    finish_row<D>(s_part[0], M, L, a.ws_q + qhg * D, cur ? a.cur_k + lkv * D : nullptr,
+                  cur ? a.cur_v + lkv * D : nullptr, a.inverse_output, a.signs_left, a.signs_right, a.sqrt_d,
+                  a.out + qhg * D);
+  }
 }
 
 // ============================================================== split path stages
@@ -584,11 +711,21 @@ int device_cu_count() {
   return cus;
 }
 
-size_t workspace_bytes(int units, int hg, int head_dim, int n_splits) {
-  const size_t counters = ((static_cast<size_t>(units) * sizeof(unsigned) + 255) / 256) * 256;
-  const size_t ml = ((static_cast<size_t>(units) * n_splits * hg * sizeof(float2) + 255) / 256) * 256;
-  const size_t acc = static_cast<size_t>(units) * n_splits * hg * head_dim * sizeof(float);
-  return counters + ml + acc;
+// Workspace layout: [ml: Lq * ns * 2][acc: Lq * ns * D][q: Lq * D] floats,
+// Lq = layers * query heads, each section 256-byte aligned.
+struct WsLayout {
+  size_t ml, acc, q, total;
+};
+
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+WsLayout workspace_layout(int64_t lq, int head_dim, int n_splits) {
+  WsLayout w;
+  w.ml = 0;
+  w.acc = align256(static_cast<size_t>(lq) * n_splits * 2 * sizeof(float));
+  w.q = w.acc + align256(static_cast<size_t>(lq) * n_splits * head_dim * sizeof(float));
+  w.total = w.q + align256(static_cast<size_t>(lq) * head_dim * sizeof(float));
+  return w;
 }
 
 // Fills the split plan; tokens per split are a multiple of 256 rows so every
@@ -686,8 +823,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   if (rc) return rc;
 
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  const size_t counters = ((static_cast<size_t>(p.units) * sizeof(unsigned) + 255) / 256) * 256;
-  const size_t ml = ((static_cast<size_t>(p.units) * p.n_splits * p.hg * sizeof(float2) + 255) / 256) * 256;
+  const WsLayout wl = workspace_layout(static_cast<int64_t>(num_layers) * query_heads, head_dim, p.n_splits);
 
   DecodeArgs a{};
   a.q = query;
@@ -713,11 +849,26 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   a.cur_v = cur_v;
   a.n_splits = p.n_splits;
   a.split_len = p.split_len;
-  a.counters = reinterpret_cast<unsigned*>(ws);
-  a.ws_ml = reinterpret_cast<float2*>(ws + counters);
-  a.ws_acc = reinterpret_cast<float*>(ws + counters + ml);
+  a.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
+  a.ws_acc = reinterpret_cast<float*>(ws + wl.acc);
+  a.ws_q = reinterpret_cast<float*>(ws + wl.q);
   a.out = out;
   const int nblk = p.units * p.n_splits;
+  MergeArgs m{};
+  m.query_heads = query_heads;
+  m.kv_heads = kv_heads;
+  m.group = a.group;
+  m.n_splits = p.n_splits;
+  m.ws_ml = a.ws_ml;
+  m.ws_acc = a.ws_acc;
+  m.ws_q = a.ws_q;
+  m.cur_k = cur_k;
+  m.cur_v = cur_v;
+  m.signs_left = signs_left;
+  m.signs_right = signs_right;
+  m.sqrt_d = a.sqrt_d;
+  m.inverse_output = a.inverse_output;
+  m.out = out;
 
   switch (fmt) {
     case 2:
@@ -739,7 +890,21 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
       return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(fmt));
   }
   if (rc) return rc;
-  return launch_status("decode_kernel");
+  rc = launch_status("decode_kernel");
+  if (rc || p.n_splits == 1) return rc;
+  const unsigned mblk = static_cast<unsigned>(static_cast<int64_t>(num_layers) * query_heads);
+  switch (head_dim) {
+    case 64:
+      hipLaunchKernelGGL(merge_kernel<64>, dim3(mblk), dim3(kBlock), 0, stream, m);
+      break;
+    case 128:
+      hipLaunchKernelGGL(merge_kernel<128>, dim3(mblk), dim3(kBlock), 0, stream, m);
+      break;
+    default:
+      hipLaunchKernelGGL(merge_kernel<256>, dim3(mblk), dim3(kBlock), 0, stream, m);
+      break;
+  }
+  return launch_status("merge_kernel");
 }
 
 template <template <int> class Body, typename... Args>
@@ -1044,13 +1209,14 @@ int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int 
 size_t tq_decode_workspace_bytes(int num_layers, int kv_heads, int query_heads, int head_dim, int n_splits,
                                  int num_cus) {
   if (num_layers <= 0 || kv_heads <= 0 || query_heads <= 0 || query_heads % kv_heads != 0) return 0;
+  if (!valid_head_dim(head_dim)) return 0;
   const int group = query_heads / kv_heads;
   const int hg = pick_hg(group);
   const int units = num_layers * kv_heads * (group / hg);
   int ns = n_splits;
   if (ns <= 0) ns = default_splits(units, static_cast<int64_t>(kMaxSplits) * kMinTokensPerSplit, num_cus);
   ns = std::min(ns, kMaxSplits);
-  return workspace_bytes(units, hg, head_dim, ns);
+  return workspace_layout(static_cast<int64_t>(num_layers) * query_heads, head_dim, ns).total;
 }
 
 int tq_decode(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads, int head_dim,

@@ -29,6 +29,42 @@ __device__ __forceinline__ float to_f32<__half>(__half v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Relaxed agent-scope atomic store / load: coherent across all XCDs of the
+// device without a full L2 writeback or invalidate.  Used to hand split-K
+// partials from one workgroup to another inside a launch.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane moves inside 16-lane rows (DPP; no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;   // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;       // lane i <-> 15 - i within 16
+
+// Sum over aligned groups of N lanes (N a power of two up to 64); every lane
+// of a group receives the group total.  After the two quad steps each quad
+// holds its sum; the mirror steps then pair a quad (half row) with the
+// other quad (half row) of the same 8 (16) lanes.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (N >= 2) v += dpp_move<kDppXor1>(v);
+  if constexpr (N >= 4) v += dpp_move<kDppXor2>(v);
+  if constexpr (N >= 8) v += dpp_move<kDppHalfMirror>(v);
+  if constexpr (N >= 16) v += dpp_move<kDppMirror>(v);
+  if constexpr (N >= 32) v += __shfl_xor(v, 16);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
 // ---------------------------------------------------------------------------
 // Walsh-Hadamard transform of one D-vector held by a wavefront.
 //
