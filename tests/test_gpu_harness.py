@@ -1,0 +1,42 @@
+"""The benchmark harnesses run end to end on the GPU (small sizes)."""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def test_synthetic_benchmark_keys_and_error(hip_device):
+    # benchmarking.py:24-86 keys; C1 shape
+    from torque_hip.benchmarking import run_synthetic_decode_benchmark
+
+    out = run_synthetic_decode_benchmark(seq_len=512, head_dim=128, kv_heads=8, bit_width=4, seed=0)
+    for key in ("seq_len", "naive_quantized_decode_ms", "ttft_proxy_ms", "reference_decode_ms", "kv_bytes_per_token",
+                "max_abs_error_vs_rotated_reference", "decode_kernel_us", "hbm_gbps"):
+        assert key in out
+    assert out["kv_bytes_per_token"] == 16 * 4 * 8 * 2
+    # 4-bit Gaussian-codebook quantisation error of the decode output (the reference reports 0.08 at D=64)
+    assert 0.0 < out["max_abs_error_vs_rotated_reference"] < 0.5
+
+
+def test_qwen_decode_benchmark_runs(hip_device, tmp_path):
+    from torque_hip.qwen_benchmark import run_qwen_decode_runtime_benchmark
+
+    text = {"model_type": "qwen3_5", "hidden_size": 1024, "head_dim": 256, "num_hidden_layers": 4,
+            "num_attention_heads": 8, "num_key_value_heads": 2, "layer_types": ["linear_attention"] * 3 + ["full_attention"]}
+    (tmp_path / "config.json").write_text(json.dumps({"model_type": "qwen3_5", "text_config": text}))
+    payload = run_qwen_decode_runtime_benchmark(model_dir=tmp_path, prefill_tokens=300, decode_steps=6, seed=1).to_dict()
+    assert payload["decode_steps"] == 6 and payload["torque_mlx_tokens_per_sec"] > 0
+    # the packed decode stays close to the fp16-dense attention on uniform(-1, 1) data
+    assert payload["max_abs_error_torque_vs_fp16"] < 0.25
+
+
+def test_cli_synthetic(hip_device, capsys):
+    from torque_hip import cli
+
+    assert cli.main(["benchmark", "synthetic", "--seq-len", "64", "--head-dim", "64", "--kv-heads", "2"]) == 0
+    assert json.loads(capsys.readouterr().out)["seq_len"] == 64.0

@@ -85,6 +85,19 @@ class TorqueKVCache:
         self._store.append(keys.unsqueeze(2), values.unsqueeze(2), rotate_keys=True, rotate_values=True)
         self.sequence_length += 1
 
+    def append_many(self, *, key: Any, value: Any) -> None:
+        """Bulk append of S tokens, keys/values [L, Hkv, S, D]; same codes as S single appends."""
+        cfg = self.config
+        shape = shape_of(key)
+        if len(shape) != 4 or shape[:2] != (cfg.num_layers, cfg.kv_heads) or shape[3] != cfg.head_dim:
+            raise ValueError(f"key must have shape ({cfg.num_layers}, {cfg.kv_heads}, seq_len, {cfg.head_dim}), got {shape}")
+        if shape_of(value) != shape:
+            raise ValueError(f"key/value sequence dimensions must match, got {shape} and {shape_of(value)}")
+        keys = to_device(key, self._store.device)
+        values = to_device(value, self._store.device)
+        self._store.append(keys, values, rotate_keys=True, rotate_values=True)
+        self.sequence_length += shape[2]
+
     def decode(self, *, query: Any) -> np.ndarray:
         """Packed decode attention for one query step (cache.py:98-140)."""
         out = self.decode_device(query=query)
