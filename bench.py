@@ -123,6 +123,21 @@ def cpu_baseline(q, k_codes, v_codes, cache, head_subset: int, budget_s: float, 
     return per_step, len(times), err, rel
 
 
+def measured_traffic(kernel: str, workload: str) -> tuple[int | None, str | None]:
+    """HBM bytes per launch of `kernel` on `workload`, from a committed rocprofv3 PMC summary.
+
+    The summaries under profiles/ carry a line
+    ``traffic_bytes_per_launch: <kernel> <workload> <bytes>`` (FETCH_SIZE and
+    WRITE_SIZE passes, each scaled by the same counter on a copy of known size).
+    """
+    for path in sorted((REPO / "profiles").glob("*hbm_traffic*.md")):
+        for line in path.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 4 and parts[0] == "traffic_bytes_per_launch:" and parts[1:3] == [kernel, workload]:
+                return int(parts[3]), f"profiles/{path.name}"
+    return None, None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -135,6 +150,12 @@ def main() -> int:
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--splits", type=int, default=0, help="split count (0 = library default)")
+    ap.add_argument(
+        "--calibration-copy-mib",
+        type=int,
+        default=0,
+        help="also run 5 device copies of this many MiB (the known-size kernel that scales PMC byte counters)",
+    )
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -225,6 +246,8 @@ def main() -> int:
     kern_us = float(np.mean(kern_ms) * 1e3)
     kern_med_us = float(np.median(kern_ms) * 1e3)
     achieved = algo_bytes / (kern_us * 1e-6) / 1e9
+    kernel_name = f"decode_kernel<PackedB{bits},{d},4>"
+    traffic, traffic_src = measured_traffic(kernel_name, args.workload)
     log(f"decode kernel mean {kern_us:.2f} us (median {kern_med_us:.2f}), wall {ms_per_step * 1e3:.2f} us/step")
 
     result = {
@@ -261,8 +284,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
-            "kernel": f"decode_kernel<PackedB{bits},{d},4>",
+            "traffic": traffic,
+            "traffic_source": traffic_src,
+            "kernel": kernel_name,
             "algorithmic_bytes_per_launch": algo_bytes,
         },
     }
@@ -313,6 +337,16 @@ def main() -> int:
         }
         result["parity_vs_oracle"] = {"max_abs": err, "rel_l2": rel, "heads_checked": subset * (hq // hkv)}
         log(f"cpu baseline {per_step * 1e6:.0f} us/step; parity max-abs {err:.2e} rel-L2 {rel:.2e}")
+
+    if args.calibration_copy_mib > 0:
+        n = args.calibration_copy_mib * 2**20 // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = n * 4
+        del src, dst
 
     print(json.dumps(result), flush=True)
     return 0

@@ -167,3 +167,20 @@ def test_cli_parser():
     assert args.benchmark_command == "qwen-decode" and args.decode_tail_capacity == 96
     syn = cli.build_parser().parse_args(["benchmark", "synthetic"])
     assert (syn.seq_len, syn.head_dim, syn.kv_heads, syn.bit_width, syn.seed) == (512, 128, 8, 4, 0)
+
+
+def test_bench_reads_committed_traffic_and_refuses_multi_gpu():
+    import importlib.util
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    spec = importlib.util.spec_from_file_location("bench_under_test", root / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    traffic, src = bench.measured_traffic("decode_kernel<PackedB4,128,4>", "M")
+    assert src and src.startswith("profiles/") and 32 * 2**20 <= traffic <= 40 * 2**20
+    assert bench.measured_traffic("decode_kernel<PackedB4,128,4>", "no-such-workload") == (None, None)
+    proc = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert proc.returncode == 2 and "one GPU" in proc.stderr
