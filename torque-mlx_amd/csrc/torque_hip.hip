@@ -10,10 +10,12 @@
 //   unpack_kernel        packed slab -> dense float32 centroid values
 //   decode_kernel<Fmt>   split-K decode attention: each workgroup owns one
 //                        (layer, KV head, query-head group) and one contiguous
-//                        sequence split; the last workgroup of a group merges
-//                        all splits (log-sum-exp) and applies the inverse
-//                        rotation.  Fmt selects packed 2/3/4-bit or dense
+//                        sequence split and writes its partial (max, sum,
+//                        accumulator); with a single split it finishes the
+//                        rows itself.  Fmt selects packed 2/3/4-bit or dense
 //                        fp16/fp32 rows.
+//   merge_kernel         log-sum-exp merge of the splits of one query head,
+//                        current token, normalisation, inverse rotation.
 //   score / softmax / accumulate kernels   the three stages of the
 //                        reference's split path, for profiling and the op API.
 
@@ -24,6 +26,7 @@
 #include <cmath>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "torque_hip.h"
 #include "tq_device.hpp"
@@ -67,7 +70,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;
 constexpr int kMaxSplits = 256;
 constexpr int kTokensPerIter = 2;  // tokens per lane group per loop iteration
-constexpr int kPrefetchIters = 2;  // loop iterations whose loads are in flight ahead
+constexpr int kPrefetchIters = 1;  // loop iterations whose loads are in flight ahead
 
 // ============================================================== rotation
 
@@ -216,13 +219,47 @@ __device__ __forceinline__ void finish_row(const float* A, float M, float L, con
   for (int i = 0; i < E; ++i) dst[lane * E + i] = e[i];
 }
 
-template <class Fmt, int D, int HG>
+// One reduce-scatter step over lane pairs (i, i xor LM): the lower lane of a
+// pair gets x_i + x_partner, the upper lane y_i + y_partner.
+template <int LM>
+__device__ __forceinline__ float scatter_pair(float x, float y, int lane) {
+  if constexpr (LM == 16 || LM == 32) {
+    const LanePair r = permlane_swap<LM>(x, y);
+    return r.first + r.second;
+  } else if constexpr (LM == 8) {
+    const float sx = x + dpp_move<kDppRor8>(x);
+    const float sy = y + dpp_move<kDppRor8>(y);
+    return (lane & 8) ? sy : sx;
+  } else {
+    const bool upper = (lane & LM) != 0;
+    const float send = upper ? x : y;
+    const float keep = upper ? y : x;
+    return keep + __shfl_xor(send, LM);
+  }
+}
+
+// Reduce-scatter of buf[0, 2*LEN) over the lanes that differ in lane bits
+// LM, LM/2, ..., LO (one step per bit, highest first): each step halves the
+// live length, the upper lane of a pair keeping the upper half.  Afterwards a
+// lane holds, summed over its partners, the chunk of the original buffer that
+// its lane bits LO..LM select (bit LM weighs half the buffer).
+template <int LO, int LM, int LEN, int NV>
+__device__ __forceinline__ void reduce_scatter(float (&buf)[NV], int lane) {
+#pragma unroll
+  for (int k = 0; k < LEN; ++k) buf[k] = scatter_pair<LM>(buf[k], buf[k + LEN], lane);
+  if constexpr (LM > LO) reduce_scatter<LO, LM / 2, LEN / 2, NV>(buf, lane);
+}
+
+template <class Fmt, int D, int HG, bool QF16>
 __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   constexpr int SD = Fmt::kSliceDims;
   constexpr int LPT = D / SD;        // lanes per token
   constexpr int TPW = kWave / LPT;   // tokens (lane groups) per wavefront
   constexpr int TPB = kWavesPerBlock * TPW;
   constexpr int U = kTokensPerIter;
+  constexpr int PF = kPrefetchIters;
+  constexpr int NB = PF + 1;         // ring of iteration slots
+  constexpr int STRIDE = U * TPB;    // tokens per workgroup iteration
   constexpr int E = D / kWave;
   constexpr int ROW = Fmt::template row_bytes<D>();
   constexpr int NV = HG * SD;        // accumulator values per lane
@@ -251,209 +288,312 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   const int layer = lkv / a.kv_heads, kvh = lkv - layer * a.kv_heads;
   const int qh0 = kvh * a.group + hg * HG;
 
+  // ---- tokens of this wavefront.  Lane group gi takes tokens
+  // first + gi + u * TPB + i * STRIDE (u < U) in iteration i: one wavefront
+  // load covers TPW consecutive rows.  Token offsets are 32-bit (the host
+  // keeps capacity * ROW below 2^31).  Every iteration but the last is full.
+  const int64_t t0 = static_cast<int64_t>(split) * a.split_len;
+  const int t1 = static_cast<int>(min(a.seq_len, t0 + a.split_len));
+  const int first = static_cast<int>(t0) + wave * TPW;
+  const int n_iter = first < t1 ? (t1 - first + STRIDE - 1) / STRIDE : 0;  // uniform per wavefront
+  const uint8_t* kbase = a.k + static_cast<int64_t>(lkv) * a.cap * ROW;
+  const uint8_t* vbase = a.v + static_cast<int64_t>(lkv) * a.cap * ROW;
+
+  // Rows past the end of the split are clamped to its last row and masked
+  // out when processed, so loads need no branch.
+  auto load_iter = [&](int i, Raw (&kr)[U], Raw (&vr)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = min(first + i * STRIDE + u * TPB + gi, t1 - 1);
+      kr[u] = Fmt::load(kbase + t * ROW, slice);
+      vr[u] = Fmt::load(vbase + t * ROW, slice);
+    }
+  };
+
+  // ---- set-up loads first: this thread's centroid-table entry, the query
+  // row and its rotation signs.  Loads complete in order, so waiting for
+  // these below does not wait for the K/V rows requested after them.
+  typename Fmt::LutT lut_kv[2];
+  if constexpr (Fmt::kHasLut) {
+    static_assert(Fmt::kLutEntries <= kBlock, "one table entry per thread");
+    if (tid < Fmt::kLutEntries) {
+      lut_kv[0] = Fmt::lut_entry(tid, a.cent_k);
+      lut_kv[1] = Fmt::lut_entry(tid, a.cent_v);
+    }
+  }
+  // Query bits are loaded raw and converted after the K/V requests below, so
+  // the conversion does not hold those requests back.
+  // A lane's query values as raw 32-bit words: E floats, or (E + 1) / 2 words
+  // of fp16 pairs.
+  float qe[E], sg_first[E], sg_second[E];
+  uint32_t qw[E];
+  if (wave < HG) {
+    const int64_t qoff = (static_cast<int64_t>(layer) * a.query_heads + qh0 + wave) * D + lane * E;
+    if constexpr (!QF16) {
+      const uint32_t* q = static_cast<const uint32_t*>(a.q) + qoff;
+#pragma unroll
+      for (int i = 0; i < E; ++i) qw[i] = q[i];
+    } else if constexpr (E == 1) {
+      qw[0] = static_cast<const unsigned short*>(a.q)[qoff];
+    } else {
+      const uint32_t* q = reinterpret_cast<const uint32_t*>(static_cast<const unsigned short*>(a.q) + qoff);
+#pragma unroll
+      for (int i = 0; i < E / 2; ++i) qw[i] = q[i];
+    }
+    if (a.rotate_query) {
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        sg_first[i] = a.signs_right[lane * E + i];
+        sg_second[i] = a.signs_left[lane * E + i];
+      }
+    }
+  }
+
+  // Software pipeline over a ring of NB = PF + 1 iteration slots: the loads of
+  // iteration i + PF are in flight while iteration i is processed.  The first
+  // PF iterations are requested here, so their latency overlaps the set-up.
+  Raw kr[NB][U], vr[NB][U];
+#pragma unroll
+  for (int j = 0; j < PF; ++j)
+    if (j < n_iter) load_iter(j, kr[j], vr[j]);
+
   // ---- centroid tables
   if constexpr (Fmt::kHasLut) {
-    for (int e = tid; e < Fmt::kLutEntries; e += kBlock) {
-      s_lut[0][e] = Fmt::lut_entry(e, a.cent_k);
-      s_lut[1][e] = Fmt::lut_entry(e, a.cent_v);
+    if (tid < Fmt::kLutEntries) {
+      s_lut[0][tid] = lut_kv[0];
+      s_lut[1][tid] = lut_kv[1];
     }
   }
 
   // ---- queries: optional rotation (bit-identical to the reference), then
   // the softmax scale and log2(e) folded in, so scores are in log2 units.
   if (wave < HG) {
-    float e[E];
-    const int64_t qoff = (static_cast<int64_t>(layer) * a.query_heads + qh0 + wave) * D + lane * E;
-    if (a.q_f16) {
-      const __half* q = static_cast<const __half*>(a.q) + qoff;
 #pragma unroll
-      for (int i = 0; i < E; ++i) e[i] = __half2float(q[i]);
-    } else {
-      const float* q = static_cast<const float*>(a.q) + qoff;
+    for (int i = 0; i < E; ++i)
+      qe[i] = QF16 ? __half2float(__ushort_as_half(static_cast<unsigned short>(qw[i / 2] >> (16 * (i % 2)))))
+                   : __builtin_bit_cast(float, qw[i]);
+    if (a.rotate_query) wave_rotate_signs<D>(qe, sg_first, sg_second, a.sqrt_d);
 #pragma unroll
-      for (int i = 0; i < E; ++i) e[i] = q[i];
-    }
-    if (a.rotate_query) wave_rotate<D>(e, a.signs_right, a.signs_left, a.sqrt_d);
-#pragma unroll
-    for (int i = 0; i < E; ++i) s_q[wave][lane * E + i] = e[i] * a.q_scale;
+    for (int i = 0; i < E; ++i) s_q[wave][lane * E + i] = qe[i] * a.q_scale;
   }
   __syncthreads();
 
+  // ---- head slots.  With HG == 4 and U == 2 the softmax runs in quad mode
+  // (see process): each lane exponentiates only the pairs (token, head) of
+  // its quad position, and the lanes of every odd quad keep their per-head
+  // registers (query slice, accumulators, running maxima) in the order
+  // h ^ 3.  The row_half_mirror / row_mirror exchanges pair quad position p
+  // with position 3 - p of a neighbouring quad, so with that order a lane
+  // always meets the partner that holds the same head.  slot s of a lane
+  // holds head s ^ slot_x.
+  constexpr bool kQuad = HG == 4 && U == 2;
+  const int q4 = lane & 3;
+  const int slot_x = (kQuad && LPT >= 8 && ((lane >> 2) & 1)) ? 3 : 0;
+
   float qv[HG][SD];
 #pragma unroll
-  for (int h = 0; h < HG; ++h)
+  for (int s = 0; s < HG; ++s)
 #pragma unroll
-    for (int i = 0; i < SD; ++i) qv[h][i] = s_q[h][slice * SD + i];
+    for (int i = 0; i < SD; ++i) qv[s][i] = s_q[s ^ slot_x][slice * SD + i];
 
   float m[HG], lsum[HG], acc[HG][SD];
 #pragma unroll
-  for (int h = 0; h < HG; ++h) {
-    m[h] = -INFINITY;
-    lsum[h] = 0.f;
+  for (int s = 0; s < HG; ++s) {
+    m[s] = -INFINITY;
+    lsum[s] = 0.f;  // quad mode uses lsum[0] for the lane's own slot q4
 #pragma unroll
-    for (int i = 0; i < SD; ++i) acc[h][i] = 0.f;
+    for (int i = 0; i < SD; ++i) acc[s][i] = 0.f;
   }
+  float m_own = -INFINITY;  // quad mode: m[q4]
 
-  // ---- main loop.  Wavefront `wave`, lane group `gi` takes tokens
-  // t0 + wave*TPW + gi + k*TPB: one wavefront load covers TPW consecutive
-  // rows.  Each iteration handles U tokens per lane group: U x HG partial
-  // scores, one group reduction (DPP), one softmax update, U value updates.
-  const int64_t t0 = static_cast<int64_t>(split) * a.split_len;
-  const int64_t t1 = min(a.seq_len, t0 + a.split_len);
-  const uint8_t* kbase = a.k + static_cast<int64_t>(lkv) * a.cap * ROW;
-  const uint8_t* vbase = a.v + static_cast<int64_t>(lkv) * a.cap * ROW;
   const typename Fmt::LutT* lut_k = s_lut[0];
   const typename Fmt::LutT* lut_v = s_lut[1];
 
-  auto load_iter = [&](int64_t base, Raw (&kr)[U], Raw (&vr)[U]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t t = base + u * TPB + gi;
-      if (t < t1) {
-        const int off = static_cast<int>(t * ROW);
-        kr[u] = Fmt::load(kbase + off, slice);
-        vr[u] = Fmt::load(vbase + off, slice);
-      } else {
-        kr[u] = Raw{};
-        vr[u] = Raw{};
-      }
-    }
-  };
-
-  auto process = [&](const Raw (&kr)[U], const Raw (&vr)[U], int64_t base) {
-    float s[U][HG];
+  // Partial dot products of this lane's slice: part[u][s] for token u, slot s.
+  auto partial_scores = [&](const Raw (&kr)[U], float (&part)[U][HG]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float x[SD];
       Fmt::decode(kr[u], slice, lut_k, x);
 #pragma unroll
-      for (int h = 0; h < HG; ++h) {
-        float d0 = 0.f, d1 = 0.f;
+      for (int s = 0; s < HG; ++s) {
+        float d = 0.f;
 #pragma unroll
-        for (int i = 0; i < SD; i += 2) {
-          d0 = fmaf(qv[h][i], x[i], d0);
-          d1 = fmaf(qv[h][i + 1], x[i + 1], d1);
-        }
-        s[u][h] = d0 + d1;
+        for (int k = 0; k < SD; ++k) d = fmaf(qv[s][k], x[k], d);
+        part[u][s] = d;
       }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int h = 0; h < HG; ++h) s[u][h] = group_sum<LPT>(s[u][h]);
-    bool valid[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) valid[u] = base + u * TPB + gi < t1;
-#pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < U; ++u) mx = valid[u] ? fmaxf(mx, s[u][h]) : mx;
-      if (mx > m[h] + kRescaleThreshold) {
-        const float alpha = fast_exp2(m[h] - mx);
-        lsum[h] *= alpha;
-#pragma unroll
-        for (int i = 0; i < SD; ++i) acc[h][i] *= alpha;
-        m[h] = mx;
-      }
-    }
-    float p[U][HG];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int h = 0; h < HG; ++h) {
-        p[u][h] = valid[u] ? fast_exp2(s[u][h] - m[h]) : 0.f;
-        lsum[h] += p[u][h];
-      }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float x[SD];
-      Fmt::decode(vr[u], slice, lut_v, x);
-#pragma unroll
-      for (int h = 0; h < HG; ++h)
-#pragma unroll
-        for (int i = 0; i < SD; ++i) acc[h][i] = fmaf(p[u][h], x[i], acc[h][i]);
     }
   };
 
-  {
-    // Software pipeline over a ring of NB = PF + 1 iteration slots: the loads
-    // of iteration i + PF are issued before iteration i is processed.
-    constexpr int PF = kPrefetchIters;
-    constexpr int NB = PF + 1;
-    const int64_t first = t0 + wave * TPW;
-    const int64_t stride = static_cast<int64_t>(U) * TPB;
-    const int64_t n_iter = first < t1 ? (t1 - first + stride - 1) / stride : 0;  // uniform per wavefront
-    Raw kr[NB][U], vr[NB][U];
+  // One iteration: U tokens per lane group -- U x HG partial scores, their
+  // reduction over the group's lanes, one online-softmax update per head and
+  // U value updates.  FULL iterations skip the validity masks.
+  auto process = [&](const Raw (&kr)[U], const Raw (&vr)[U], int i, auto full) {
+    constexpr bool FULL = decltype(full)::value;
+    bool valid[U];
 #pragma unroll
-    for (int j = 0; j < PF; ++j) load_iter(first + j * stride, kr[j], vr[j]);
-    for (int64_t it = 0; it < n_iter; it += NB) {
+    for (int u = 0; u < U; ++u) valid[u] = FULL || first + i * STRIDE + u * TPB + gi < t1;
+    float part[U][HG];
+    partial_scores(kr, part);
+    // Value rows are decoded (LDS table reads issued) before the softmax so
+    // the table latency overlaps it.
+    float xv[U][SD];
 #pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        if (it + j >= n_iter) break;
-        const int64_t base = first + (it + j) * stride;
-        load_iter(base + PF * stride, kr[(j + PF) % NB], vr[(j + PF) % NB]);
-        process(kr[j], vr[j], base);
+    for (int u = 0; u < U; ++u) Fmt::decode(vr[u], slice, lut_v, xv[u]);
+    if constexpr (kQuad) {
+      // Reduce-scatter inside the quad (DPP xor 2, then xor 1): quad
+      // position q4 ends with the quad's sum for slot q4 of both tokens; the
+      // other quads of the group are added after.  Then each lane
+      // exponentiates its two pairs and the value update takes every pair's
+      // weight from the quad lane that owns it (quad_perm broadcast).
+      float own[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool hi = (q4 & 2) != 0;
+        const float r0 = (hi ? part[u][2] : part[u][0]) + dpp_move<kDppXor2>(hi ? part[u][0] : part[u][2]);
+        const float r1 = (hi ? part[u][3] : part[u][1]) + dpp_move<kDppXor2>(hi ? part[u][1] : part[u][3]);
+        const bool odd = (q4 & 1) != 0;
+        own[u] = cross_quad_sum<LPT>((odd ? r1 : r0) + dpp_move<kDppXor1>(odd ? r0 : r1));
       }
+      bool need = false;
+#pragma unroll
+      for (int u = 0; u < U; ++u) need = need || (valid[u] && own[u] > m_own + kRescaleThreshold);
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        // Some running maximum moves (first iteration, rare afterwards).
+#pragma unroll
+        for (int s = 0; s < HG; ++s) {
+          float mx = -INFINITY;
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const float v = quad_broadcast(own[u], s);
+            mx = valid[u] ? fmaxf(mx, v) : mx;
+          }
+          if (mx > m[s] + kRescaleThreshold) {
+            const float alpha = fast_exp2(m[s] - mx);
+#pragma unroll
+            for (int k = 0; k < SD; ++k) acc[s][k] *= alpha;
+            if (q4 == s) lsum[0] *= alpha;
+            m[s] = mx;
+          }
+        }
+        m_own = q4 == 0 ? m[0] : q4 == 1 ? m[1] : q4 == 2 ? m[2] : m[3];
+      }
+      float p_own[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        p_own[u] = valid[u] ? fast_exp2(own[u] - m_own) : 0.f;
+        lsum[0] += p_own[u];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int s = 0; s < HG; ++s) {
+          const float p = quad_broadcast(p_own[u], s);
+#pragma unroll
+          for (int k = 0; k < SD; ++k) acc[s][k] = fmaf(p, xv[u][k], acc[s][k]);
+        }
+    } else {
+      // Every lane of the group reduces and exponentiates every pair.
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int s = 0; s < HG; ++s) part[u][s] = group_sum<LPT>(part[u][s]);
+#pragma unroll
+      for (int s = 0; s < HG; ++s) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < U; ++u) mx = valid[u] ? fmaxf(mx, part[u][s]) : mx;
+        if (mx > m[s] + kRescaleThreshold) {
+          const float alpha = fast_exp2(m[s] - mx);
+          lsum[s] *= alpha;
+#pragma unroll
+          for (int k = 0; k < SD; ++k) acc[s][k] *= alpha;
+          m[s] = mx;
+        }
+      }
+      float p[U][HG];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int s = 0; s < HG; ++s) {
+          p[u][s] = valid[u] ? fast_exp2(part[u][s] - m[s]) : 0.f;
+          lsum[s] += p[u][s];
+        }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int s = 0; s < HG; ++s)
+#pragma unroll
+          for (int k = 0; k < SD; ++k) acc[s][k] = fmaf(p[u][s], xv[u][k], acc[s][k]);
+    }
+  };
+
+  for (int it = 0; it < n_iter; it += NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int i = it + j;
+      if (i >= n_iter) break;
+      if (i + PF < n_iter) load_iter(i + PF, kr[(j + PF) % NB], vr[(j + PF) % NB]);
+      if (first + i * STRIDE + (U - 1) * TPB + TPW <= t1)
+        process(kr[j], vr[j], i, std::true_type{});
+      else
+        process(kr[j], vr[j], i, std::false_type{});
     }
   }
 
   // ---- combine the lane groups of this workgroup (log-sum-exp).
-  // Workgroup max per head, then every lane rescales to it.
-  float M[HG];
+  // Softmax sums per slot: in quad mode each quad position holds its own
+  // slot's sum.  m and these sums are equal on the lanes of a group that
+  // share slot_x, and lanes that share a slice share slot_x, so reducing over
+  // the lanes of one slice covers every group once.  Lane 0 has slot_x = 0.
+  float ls[HG];
 #pragma unroll
-  for (int h = 0; h < HG; ++h) {
-    float mw = m[h];
+  for (int s = 0; s < HG; ++s) {
+    if constexpr (kQuad)
+      ls[s] = group_sum<4>(q4 == s ? lsum[0] : 0.f);
+    else
+      ls[s] = lsum[s];
+  }
 #pragma unroll
-    for (int mask = LPT; mask < kWave; mask <<= 1) mw = fmaxf(mw, __shfl_xor(mw, mask));
-    if (lane == 0) s_mw[wave][h] = mw;
+  for (int s = 0; s < HG; ++s) {
+    const float mw = strided_reduce<LPT, OpMax>(m[s]);
+    if (lane == 0) s_mw[wave][s] = mw;
   }
   __syncthreads();
+  float buf[NV];
+#pragma unroll
+  for (int s = 0; s < HG; ++s) {
+    const int h = s ^ slot_x;
+    float M = s_mw[0][h];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) M = fmaxf(M, s_mw[w][h]);
+    const float f = ls[s] > 0.f ? fast_exp2(m[s] - M) : 0.f;
+    const float lw = strided_reduce<LPT, OpSum>(ls[s] * f);
+    if (lane == 0) s_lw[wave][s] = lw;
+#pragma unroll
+    for (int k = 0; k < SD; ++k) buf[s * SD + k] = acc[s][k] * f;
+  }
+  // Reduce-scatter the accumulators over the TPW lane groups of the
+  // wavefront: afterwards lane (gi, slice) holds values
+  // [gi * NV / TPW, (gi + 1) * NV / TPW) of its slice, summed over groups.
+  if constexpr (TPW > 1) reduce_scatter<LPT, kWave / 2, NV / 2, NV>(buf, lane);
+  {
+    constexpr int W = NV / TPW;
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const int v = gi * W + k;
+      const int s = v / SD, d = v - s * SD;
+      s_red[wave][(s ^ slot_x) * D + slice * SD + d] = buf[k];
+    }
+  }
+  __syncthreads();
+  float M[HG];  // workgroup maximum of each head
 #pragma unroll
   for (int h = 0; h < HG; ++h) {
     M[h] = s_mw[0][h];
 #pragma unroll
     for (int w = 1; w < kWavesPerBlock; ++w) M[h] = fmaxf(M[h], s_mw[w][h]);
   }
-  float buf[NV];
-#pragma unroll
-  for (int h = 0; h < HG; ++h) {
-    const float f = lsum[h] > 0.f ? fast_exp2(m[h] - M[h]) : 0.f;
-    float lw = lsum[h] * f;
-#pragma unroll
-    for (int mask = LPT; mask < kWave; mask <<= 1) lw += __shfl_xor(lw, mask);
-    if (lane == 0) s_lw[wave][h] = lw;
-#pragma unroll
-    for (int i = 0; i < SD; ++i) buf[h * SD + i] = acc[h][i] * f;
-  }
-  // Reduce-scatter the accumulators over the TPW lane groups of the
-  // wavefront: afterwards lane (gi, slice) holds values
-  // [gi * NV / TPW, (gi + 1) * NV / TPW) of its slice, summed over groups.
-  {
-    int len = NV;
-#pragma unroll
-    for (int gm = TPW / 2; gm >= 1; gm >>= 1) {
-      const int lm = gm * LPT;
-      const bool upper = (lane & lm) != 0;
-      len >>= 1;
-#pragma unroll
-      for (int k = 0; k < NV / 2; ++k) {
-        if (k < len) {
-          const float send = upper ? buf[k] : buf[k + len];
-          const float keep = upper ? buf[k + len] : buf[k];
-          buf[k] = keep + __shfl_xor(send, lm);
-        }
-      }
-    }
-    constexpr int W = NV / TPW;
-#pragma unroll
-    for (int k = 0; k < W; ++k) {
-      const int v = gi * W + k;
-      const int h = v / SD, i = v - h * SD;
-      s_red[wave][h * D + slice * SD + i] = buf[k];
-    }
-  }
-  __syncthreads();
 
   // ---- one split: this workgroup holds the whole result and finishes it.
   const int64_t qhg0 = static_cast<int64_t>(layer) * a.query_heads + qh0;
@@ -544,8 +684,7 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(const MergeArgs a) {
   const float ms = tid < ns ? ml[tid * 2] : -INFINITY;
   const float ls = tid < ns ? ml[tid * 2 + 1] : 0.f;
   float mx = ms;
-#pragma unroll
-  for (int mask = 1; mask < kWave; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask));
+  mx = group_reduce<kWave, OpMax>(mx);
   if (lane == 0) s_red[wave] = mx;
   __syncthreads();
   const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
@@ -616,8 +755,7 @@ __global__ __launch_bounds__(kBlock) void score_kernel(const float* __restrict__
 #pragma unroll
     for (int i = 0; i < SD; ++i) s = fmaf(qv[i], x[i], s);
   }
-#pragma unroll
-  for (int mask = 1; mask < LPT; mask <<= 1) s += __shfl_xor(s, mask);
+  s = group_sum<LPT>(s);
   if (t < seq_len && slice == 0) scores[static_cast<int64_t>(b) * seq_len + t] = s;
 }
 
@@ -629,14 +767,14 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(const float* __restrict
   float* orow = w + static_cast<int64_t>(blockIdx.x) * seq_len;
   float mx = -INFINITY;
   for (int64_t t = tid; t < seq_len; t += kBlock) mx = fmaxf(mx, row[t] * scale);
-  for (int mask = 1; mask < kWave; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask));
+  mx = group_reduce<kWave, OpMax>(mx);
   if (lane == 0) s_red[wave] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   __syncthreads();
   float sum = 0.f;
   for (int64_t t = tid; t < seq_len; t += kBlock) sum += expf(row[t] * scale - mx);
-  for (int mask = 1; mask < kWave; mask <<= 1) sum += __shfl_xor(sum, mask);
+  sum = group_sum<kWave>(sum);
   if (lane == 0) s_red[wave] = sum;
   __syncthreads();
   sum = s_red[0] + s_red[1] + s_red[2] + s_red[3];
@@ -752,12 +890,20 @@ int make_plan(int num_layers, int kv_heads, int query_heads, int head_dim, int64
   return TQ_OK;
 }
 
+template <class Fmt, int D, int HG, bool QF16>
+void launch_decode_q(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  if (start != nullptr || stop != nullptr)
+    hipExtLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16>), dim3(nblk), dim3(kBlock), 0, stream, start, stop, 0, a);
+  else
+    hipLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16>), dim3(nblk), dim3(kBlock), 0, stream, a);
+}
+
 template <class Fmt, int D, int HG>
 void launch_decode(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
-  if (start != nullptr || stop != nullptr)
-    hipExtLaunchKernelGGL((decode_kernel<Fmt, D, HG>), dim3(nblk), dim3(kBlock), 0, stream, start, stop, 0, a);
+  if (a.q_f16)
+    launch_decode_q<Fmt, D, HG, true>(a, nblk, stream, start, stop);
   else
-    hipLaunchKernelGGL((decode_kernel<Fmt, D, HG>), dim3(nblk), dim3(kBlock), 0, stream, a);
+    launch_decode_q<Fmt, D, HG, false>(a, nblk, stream, start, stop);
 }
 
 template <class Fmt, int D>

@@ -29,39 +29,120 @@ __device__ __forceinline__ float to_f32<__half>(__half v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Relaxed agent-scope atomic store / load: coherent across all XCDs of the
-// device without a full L2 writeback or invalidate.  Used to hand split-K
-// partials from one workgroup to another inside a launch.
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // ---------------------------------------------------------------------------
-// Cross-lane moves inside 16-lane rows (DPP; no LDS round trip).
+// Cross-lane data movement without LDS.
+//
+// DPP moves inside 16-lane rows.  Every control used here has a valid source
+// lane for every lane, so bound_ctrl changes nothing but lets the compiler
+// fold the move into the consuming VALU instruction.
 template <int CTRL>
 __device__ __forceinline__ float dpp_move(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;   // lane i <-> 7 - i within 8
 constexpr int kDppMirror = 0x140;       // lane i <-> 15 - i within 16
+constexpr int kDppRor4 = 0x124;         // lane i <- lane (i + 4) mod 16
+constexpr int kDppRor8 = 0x128;         // lane i <- lane (i + 8) mod 16, i.e. i xor 8
 
-// Sum over aligned groups of N lanes (N a power of two up to 64); every lane
-// of a group receives the group total.  After the two quad steps each quad
-// holds its sum; the mirror steps then pair a quad (half row) with the
-// other quad (half row) of the same 8 (16) lanes.
+// gfx950 v_permlane16_swap / v_permlane32_swap.  With x in the first operand
+// and y in the second, for every lane pair (i, i xor M), M = 16 or 32, i the
+// lower lane: afterwards first = (x_i, y_i) and second = (x_(i^M), y_(i^M)),
+// listing (lower lane, upper lane).  So first + second gives the lower lane
+// x_i + x_(i^M) and the upper lane y_i + y_(i^M): one reduce-scatter step;
+// with x = y it is an all-reduce step.
+struct LanePair {
+  float first, second;
+};
+template <int M>
+__device__ __forceinline__ LanePair permlane_swap(float x, float y) {
+  static_assert(M == 16 || M == 32, "permlane swaps pair lanes 16 or 32 apart");
+  const unsigned ux = __builtin_bit_cast(unsigned, x), uy = __builtin_bit_cast(unsigned, y);
+  if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(ux, uy, false, false);
+    return {__builtin_bit_cast(float, static_cast<unsigned>(r[0])), __builtin_bit_cast(float, static_cast<unsigned>(r[1]))};
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(ux, uy, false, false);
+    return {__builtin_bit_cast(float, static_cast<unsigned>(r[0])), __builtin_bit_cast(float, static_cast<unsigned>(r[1]))};
+  }
+}
+
+struct OpSum {
+  __device__ static float f(float a, float b) { return a + b; }
+};
+struct OpMax {
+  __device__ static float f(float a, float b) { return fmaxf(a, b); }
+};
+
+// All-reduce over the lane pairs (i, i xor M), M = 16 or 32.
+template <int M, class Op>
+__device__ __forceinline__ float xor_reduce(float v) {
+  const LanePair r = permlane_swap<M>(v, v);
+  return Op::f(r.first, r.second);
+}
+
+// Reduction over aligned groups of N consecutive lanes (N a power of two up
+// to 64); every lane of a group receives the group result.  After the two
+// quad steps each quad holds its result; the mirror steps then pair a quad
+// (half row) with the other quad (half row) of the same 8 (16) lanes.
+template <int N, class Op = OpSum>
+__device__ __forceinline__ float group_reduce(float v) {
+  if constexpr (N >= 2) v = Op::f(v, dpp_move<kDppXor1>(v));
+  if constexpr (N >= 4) v = Op::f(v, dpp_move<kDppXor2>(v));
+  if constexpr (N >= 8) v = Op::f(v, dpp_move<kDppHalfMirror>(v));
+  if constexpr (N >= 16) v = Op::f(v, dpp_move<kDppMirror>(v));
+  if constexpr (N >= 32) v = xor_reduce<16, Op>(v);
+  if constexpr (N >= 64) v = xor_reduce<32, Op>(v);
+  return v;
+}
 template <int N>
 __device__ __forceinline__ float group_sum(float v) {
-  if constexpr (N >= 2) v += dpp_move<kDppXor1>(v);
-  if constexpr (N >= 4) v += dpp_move<kDppXor2>(v);
+  return group_reduce<N, OpSum>(v);
+}
+
+// Value of quad position S, broadcast to every lane of each quad.
+template <int S>
+__device__ __forceinline__ float quad_broadcast_t(float v) {
+  return dpp_move<S | (S << 2) | (S << 4) | (S << 6)>(v);
+}
+__device__ __forceinline__ float quad_broadcast(float v, int s) {
+  switch (s) {
+    case 0:
+      return quad_broadcast_t<0>(v);
+    case 1:
+      return quad_broadcast_t<1>(v);
+    case 2:
+      return quad_broadcast_t<2>(v);
+    default:
+      return quad_broadcast_t<3>(v);
+  }
+}
+
+// Sum of the quads of an aligned group of N lanes (N a power of two, 4..64)
+// in which quad position p of one quad is matched with position 3 - p of the
+// neighbouring quad (row_half_mirror, row_mirror) and with the same position
+// in the other half rows (lanes 16 and 32 apart).
+template <int N>
+__device__ __forceinline__ float cross_quad_sum(float v) {
   if constexpr (N >= 8) v += dpp_move<kDppHalfMirror>(v);
   if constexpr (N >= 16) v += dpp_move<kDppMirror>(v);
-  if constexpr (N >= 32) v += __shfl_xor(v, 16);
-  if constexpr (N >= 64) v += __shfl_xor(v, 32);
+  if constexpr (N >= 32) v = xor_reduce<16, OpSum>(v);
+  if constexpr (N >= 64) v = xor_reduce<32, OpSum>(v);
+  return v;
+}
+
+// Reduction over the lanes of a wavefront that share (lane mod G), G a power
+// of two >= 4; every lane receives the result of its residue class.  Inside a
+// 16-lane row the class is closed under rotation by 4 and 8, so two rotate
+// steps cover it; the permlane steps join the rows.
+template <int G, class Op>
+__device__ __forceinline__ float strided_reduce(float v) {
+  static_assert(G >= 4 && G <= kWave && (G & (G - 1)) == 0, "stride must be a power of two in [4, 64]");
+  if constexpr (G <= 4) v = Op::f(v, dpp_move<kDppRor4>(v));
+  if constexpr (G <= 8) v = Op::f(v, dpp_move<kDppRor8>(v));
+  if constexpr (G <= 16) v = xor_reduce<16, Op>(v);
+  if constexpr (G <= 32) v = xor_reduce<32, Op>(v);
   return v;
 }
 
@@ -104,16 +185,30 @@ __device__ __forceinline__ void wave_fwht(float (&v)[D / kWave]) {
 // by float32(sqrt(D)) (correctly rounded), multiply by the second signs.
 // apply():   s_first = signs_right, s_second = signs_left
 // inverse(): s_first = signs_left,  s_second = signs_right
+// wave_rotate_signs takes this lane's E signs of each vector in registers;
+// wave_rotate loads them.
+template <int D>
+__device__ __forceinline__ void wave_rotate_signs(float (&v)[D / kWave], const float (&s_first)[D / kWave],
+                                                  const float (&s_second)[D / kWave], float sqrt_d) {
+  constexpr int E = D / kWave;
+#pragma unroll
+  for (int i = 0; i < E; ++i) v[i] = __fmul_rn(v[i], s_first[i]);
+  wave_fwht<D>(v);
+#pragma unroll
+  for (int i = 0; i < E; ++i) v[i] = __fmul_rn(__fdiv_rn(v[i], sqrt_d), s_second[i]);
+}
 template <int D>
 __device__ __forceinline__ void wave_rotate(float (&v)[D / kWave], const float* __restrict__ s_first,
                                             const float* __restrict__ s_second, float sqrt_d) {
   constexpr int E = D / kWave;
   const int base = lane_id() * E;
+  float f[E], g[E];
 #pragma unroll
-  for (int i = 0; i < E; ++i) v[i] = __fmul_rn(v[i], s_first[base + i]);
-  wave_fwht<D>(v);
-#pragma unroll
-  for (int i = 0; i < E; ++i) v[i] = __fmul_rn(__fdiv_rn(v[i], sqrt_d), s_second[base + i]);
+  for (int i = 0; i < E; ++i) {
+    f[i] = s_first[base + i];
+    g[i] = s_second[base + i];
+  }
+  wave_rotate_signs<D>(v, f, g, sqrt_d);
 }
 
 // ---------------------------------------------------------------------------
