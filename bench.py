@@ -42,7 +42,14 @@ WORKLOADS = {
     "C3": (1, 8, 32, 128, 2, 32768, 1.0, "C3: head_dim 128, 2-bit, seq_len 32768, 8 KV heads, 32 query heads"),
     "C4": (1, 2, 8, 256, 4, 131072, 0.5, "C4: head_dim 256, 4-bit, seq_len 131072, 2 KV heads, 8 query heads"),
     "C1": (1, 8, 8, 128, 4, 512, 1.0, "C1: head_dim 128, 4-bit, seq_len 512, 8 KV heads, 8 query heads"),
-    "C2": (1, 4, 16, 64, 3, 4096, 1.0, "C2: head_dim 64, 3-bit, seq_len 4096, 4 KV heads, 16 query heads"),
+}
+
+# Decode loops: prefill seq_len tokens, then `steps` steps of (append one token + decode) in every layer.
+LOOP_WORKLOADS = {
+    # name: (layers, kv_heads, query_heads, head_dim, bits, prefill, steps, std, description)
+    "C2": (1, 4, 16, 64, 3, 4096, 64, 1.0, "C2: head_dim 64, 3-bit, 4 KV / 16 query heads, prefill 4096, 64 steps"),
+    "C5": (24, 4, 16, 256, 4, 8192, 128, 1.0,
+           "C5: 24 layers, head_dim 256, 4-bit, 4 KV / 16 query heads, prefill 8192, 128 steps"),
 }
 
 
@@ -138,12 +145,188 @@ def measured_traffic(kernel: str, workload: str) -> tuple[int | None, str | None
     return None, None
 
 
+def read_ceiling(torch, _lib, hip, dev, step_bytes: int, total_mib: int) -> dict:
+    """Streaming-read ceiling of the device (tq_stream_read): one pass over `total_mib`, and reads of
+    `step_bytes` (one decode step's packed K+V) cycling through the same buffer."""
+    chunk = (step_bytes + 255) // 256 * 256
+    n_chunks = max(3, total_mib * 2**20 // chunk)
+    buf = torch.empty(n_chunks * chunk, dtype=torch.uint8, device=dev)
+    buf.view(torch.int32).random_()
+    sink = torch.empty(8 * 1024, dtype=torch.float32, device=dev)
+    fn = _lib.load().tq_stream_read
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    base = buf.data_ptr()
+    for i in range(3):
+        _lib.check(fn(base, n_chunks * chunk, sink.data_ptr(), 0, stream, None, None))
+    ev = [(hip.event(), hip.event()) for _ in range(5)]
+    for e0, e1 in ev:
+        _lib.check(fn(base, n_chunks * chunk, sink.data_ptr(), 0, stream, e0, e1))
+    torch.cuda.synchronize()
+    full_us = float(np.median([hip.elapsed_ms(a, b) for a, b in ev]) * 1e3)
+    ev = [(hip.event(), hip.event()) for _ in range(100)]
+    for i, (e0, e1) in enumerate(ev):
+        _lib.check(fn(base + (i % n_chunks) * chunk, step_bytes // 16 * 16, sink.data_ptr(), 0, stream, e0, e1))
+    torch.cuda.synchronize()
+    step_us = float(np.mean([hip.elapsed_ms(a, b) for a, b in ev]) * 1e3)
+    del buf
+    return {
+        "gbps_full_pass": round(n_chunks * chunk / (full_us * 1e-6) / 1e9, 1),
+        "full_pass_bytes": n_chunks * chunk,
+        "gbps_step_bytes": round(step_bytes / (step_us * 1e-6) / 1e9, 1),
+        "step_bytes": step_bytes,
+        "kernel": "stream_read_kernel (16-byte loads, 8 workgroups per CU)",
+    }
+
+
+def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
+    """Decode loop (C2, C5): one num_layers=1 cache per layer, as the reference's Qwen adapter builds them;
+    each step appends one token and decodes in every layer, layer after layer."""
+    L, hkv, hq, d, bits, s0, steps, std, desc = LOOP_WORKLOADS[args.workload]
+    if args.steps_given:
+        steps = args.steps
+    log(f"workload {desc} ({steps} timed steps)")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    caches = []
+    for _ in range(L):
+        cfg = th.TorqueConfig(bit_width=bits, head_dim=d, num_layers=1, kv_heads=hkv, rotation_seed=args.seed)
+        cache = th.TorqueKVCacheHIP(config=cfg, initial_capacity=s0 + steps, decode_tail_capacity=0)
+        k = torch.randn((1, hkv, s0, d), generator=g, device=dev) * std
+        k *= torch.exp(torch.randn((1, hkv, 1, d), generator=g, device=dev))
+        v = torch.randn((1, hkv, s0, d), generator=g, device=dev) * std
+        cache.append_many(key=k.half(), value=v.half())
+        caches.append(cache)
+        del k, v
+    new_k = (torch.randn((steps, L, hkv, d), generator=g, device=dev) * std).half()
+    new_v = (torch.randn((steps, L, hkv, d), generator=g, device=dev) * std).half()
+    queries = (torch.randn((steps, L, hq, d), generator=g, device=dev) * std).half()
+    torch.cuda.synchronize()
+
+    stores = [c._store for c in caches]
+    w = stores[0].layout.packed_words
+    n_splits = [ops.plan_splits(1, hkv, hq, d, s0 + steps, dev) for _ in range(L)]
+    ws = ops.workspace_for(1, hkv, hq, d, 0, dev)
+    out = torch.empty((L, hq, d), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    lib = _lib.load()
+    rot = _lib.TQ_ROTATE_KEYS | _lib.TQ_ROTATE_VALUES
+    dflags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT
+    calls = []  # per step: list of (fn, args) for every layer
+    for t in range(steps):
+        seq = s0 + t
+        step_calls = []
+        for l, st in enumerate(stores):
+            step_calls.append((lib.tq_append, (
+                new_k[t, l].data_ptr(), new_v[t, l].data_ptr(), _lib.TQ_F16, 1, hkv, 1, d, bits, st.signs_left.data_ptr(),
+                st.signs_right.data_ptr(), rot, st.key_boundaries.data_ptr(), st.value_boundaries.data_ptr(),
+                st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, seq, stream)))
+            step_calls.append((lib.tq_decode, (
+                queries[t, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d, bits, st.key_codes.data_ptr(),
+                st.value_codes.data_ptr(), st.capacity, seq + 1, st.key_centroids.data_ptr(),
+                st.value_centroids.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), dflags, None, None,
+                0, ws.data_ptr(), out[l].data_ptr(), stream)))
+        calls.append(step_calls)
+
+    # warm-up: decode-only passes over every layer at the prefill length (the caches are not changed)
+    for _ in range(args.warmup):
+        for l, st in enumerate(stores):
+            _lib.check(lib.tq_decode(queries[0, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d, bits, st.key_codes.data_ptr(),
+                                     st.value_codes.data_ptr(), st.capacity, s0, st.key_centroids.data_ptr(),
+                                     st.value_centroids.data_ptr(), st.signs_left.data_ptr(),
+                                     st.signs_right.data_ptr(), dflags, None, None, 0, ws.data_ptr(),
+                                     out[l].data_ptr(), stream))
+    # a 1 GiB read between steps evicts the slabs from the 256 MB Infinity Cache; it is outside the events
+    flush = torch.empty(2**30, dtype=torch.uint8, device=dev)
+    sink = torch.empty(8 * 1024, dtype=torch.float32, device=dev)
+    events = [(hip.event(), hip.event()) for _ in range(steps)]
+    torch.cuda.synchronize()
+    hip.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    t_start = time.perf_counter()
+    for t in range(steps):
+        _lib.check(lib.tq_stream_read(flush.data_ptr(), 2**30, sink.data_ptr(), 0, stream, None, None))
+        hip.lib.hipEventRecord(events[t][0], stream)
+        for fn, a in calls[t]:
+            rc = fn(*a)
+            if rc != 0:
+                _lib.check(rc)
+        hip.lib.hipEventRecord(events[t][1], stream)
+    torch.cuda.synchronize()
+    host_s = time.perf_counter() - t_start
+    step_us = np.array([hip.elapsed_ms(a, b) for a, b in events]) * 1e3
+    packed = [L * hkv * (s0 + t + 1) * 2 * w * 4 for t in range(steps)]
+    total_bytes = float(sum(packed))
+    mean_us = float(step_us.mean())
+    log(f"step mean {mean_us:.1f} us (median {np.median(step_us):.1f}); host enqueue {host_s / steps * 1e6:.1f} us/step")
+
+    result = {
+        "metric": f"decode-loop step latency and packed KV GB/s ({args.workload})",
+        "value": round(total_bytes / (step_us.sum() * 1e-6) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean_us / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": desc,
+            "layers": L,
+            "kv_heads": hkv,
+            "query_heads": hq,
+            "head_dim": d,
+            "bits": bits,
+            "prefill": s0,
+            "query_dtype": "f16",
+            "n_splits_at_prefill": n_splits[0],
+            "step": "per layer: tq_append (1 token) + tq_decode (split kernel + merge kernel)",
+        },
+        "step_us_mean": round(mean_us, 2),
+        "step_us_median": round(float(np.median(step_us)), 2),
+        "step_us_min": round(float(step_us.min()), 2),
+        "host_enqueue_us_per_step": round(host_s / steps * 1e6, 1),
+        "packed_bytes_last_step": packed[-1],
+    }
+    if not args.no_cpu_baseline:
+        from oracle import torque_oracle as o
+
+        st0, c0 = stores[0], caches[0]
+        kc_np = st0.key_codes[:, :, :s0].cpu().numpy().view(np.uint32)
+        vc_np = st0.value_codes[:, :, :s0].cpu().numpy().view(np.uint32)
+        q0 = queries[0, 0].float().cpu().numpy()
+        gq = hq // hkv
+        times = []
+        t_begin = time.perf_counter()
+        while time.perf_counter() - t_begin < args.cpu_budget or not times:
+            t1 = time.perf_counter()
+            q_rot = o.rotation_apply(q0, c0.rotation.signs_left, c0.rotation.signs_right)
+            idx = np.arange(hq) // gq
+            o.rotation_inverse(o.decode_packed_reference(q_rot, kc_np[0][idx], vc_np[0][idx],
+                                                         c0.key_codebook.centroids, c0.value_codebook.centroids,
+                                                         bit_width=bits, head_dim=d),
+                               c0.rotation.signs_left, c0.rotation.signs_right)
+            times.append(time.perf_counter() - t1)
+        per_step = float(np.median(times)) * L
+        result["cpu_baseline"] = {
+            "value": round(packed[0] / per_step / 1e9, 4),
+            "unit": "GB/s",
+            "us_per_step": round(per_step * 1e6, 1),
+            "cores": 1,
+            "kind": "port",
+            "sample": f"numpy oracle decode of layer 0 at the prefill length, {len(times)} repetitions, "
+            f"median scaled by {L} layers (appends not included)",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="M", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="M", choices=sorted(WORKLOADS) + sorted(LOOP_WORKLOADS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--replica-mib", type=int, default=768, help="combined size of the slab replicas cycled through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -157,6 +340,7 @@ def main() -> int:
         help="also run 5 device copies of this many MiB (the known-size kernel that scales PMC byte counters)",
     )
     args = ap.parse_args()
+    args.steps_given = "--steps" in sys.argv
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
@@ -176,6 +360,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     _lib.load()
     hip = Hip()
+    if args.workload in LOOP_WORKLOADS:
+        return run_loop(args, torch, th, _lib, ops, hip, dev)
 
     L, hkv, hq, d, bits, s, std, desc = WORKLOADS[args.workload]
     log(f"workload {desc}")
@@ -320,6 +506,12 @@ def main() -> int:
         }
         log(f"fp16-dense kernel {d_us:.2f} us, packed speedup {d_us / kern_us:.2f}x")
         del dreps, kd, vd
+
+    ceiling = read_ceiling(torch, _lib, hip, dev, packed_bytes, args.replica_mib)
+    result["hbm_read_ceiling"] = ceiling
+    result["roofline"]["frac_of_read_ceiling"] = round(achieved / ceiling["gbps_step_bytes"], 4)
+    log(f"streaming-read ceiling {ceiling['gbps_full_pass']:.0f} GB/s (full pass), "
+        f"{ceiling['gbps_step_bytes']:.0f} GB/s at {packed_bytes / 2**20:.0f} MiB per launch")
 
     if not args.no_cpu_baseline:
         kc_np = store.key_codes[:, :, :s].cpu().numpy().view(np.uint32)

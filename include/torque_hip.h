@@ -156,6 +156,16 @@ int tq_softmax_rows(const float* scores, int batch, int64_t seq_len, float scale
 int tq_accumulate_packed(const float* weights, const uint32_t* codes, int batch, int64_t seq_len, int head_dim,
                          int bits, const float* centroids, float* out, hipStream_t stream);
 
+/* Measurement helper, no counterpart in the reference: streams `bytes` bytes
+ * (a multiple of 16, 16-byte aligned) through 16-byte loads over n_blocks
+ * workgroups (<= 0: eight per compute unit) -- the device's streaming-read
+ * ceiling that the decode kernels' bandwidth is compared with.  `sink` holds
+ * n_blocks floats and is written only in the (practically impossible) case
+ * that the xor of the data equals a fixed pattern.  start/stop events (may be
+ * NULL) are bound to the kernel as in tq_decode_timed. */
+int tq_stream_read(const void* data, size_t bytes, float* sink, int n_blocks, hipStream_t stream, hipEvent_t start,
+                   hipEvent_t stop);
+
 #ifdef __cplusplus
 }
 #endif

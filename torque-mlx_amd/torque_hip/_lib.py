@@ -65,6 +65,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tq_score_packed": (_i, [_p, _p, _i, _i64, _i, _i, _p, _p, _p]),
     "tq_softmax_rows": (_i, [_p, _i, _i64, _f, _p, _p]),
     "tq_accumulate_packed": (_i, [_p, _p, _i, _i64, _i, _i, _p, _p, _p]),
+    "tq_stream_read": (_i, [_p, _sz, _p, _i, _p, _p, _p]),
 }
 
 _LIB: ctypes.CDLL | None = None
