@@ -42,6 +42,7 @@ WORKLOADS = {
     "C3": (1, 8, 32, 128, 2, 32768, 1.0, "C3: head_dim 128, 2-bit, seq_len 32768, 8 KV heads, 32 query heads"),
     "C4": (1, 2, 8, 256, 4, 131072, 0.5, "C4: head_dim 256, 4-bit, seq_len 131072, 2 KV heads, 8 query heads"),
     "C1": (1, 8, 8, 128, 4, 512, 1.0, "C1: head_dim 128, 4-bit, seq_len 512, 8 KV heads, 8 query heads"),
+    "C5L": (1, 4, 16, 256, 4, 8192, 1.0, "C5 one layer: head_dim 256, 4-bit, seq_len 8192, 4 KV heads, 16 query heads"),
 }
 
 # Decode loops: prefill seq_len tokens, then `steps` steps of (append one token + decode) in every layer.
@@ -66,6 +67,16 @@ class Hip:
         self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
         self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        self.lib.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipGraphInstantiate.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_void_p,
+                                                 ctypes.c_void_p, ctypes.c_size_t]
+        self.lib.hipGraphLaunch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipGraphExecDestroy.argtypes = [ctypes.c_void_p]
 
     def event(self) -> ctypes.c_void_p:
         ev = ctypes.c_void_p()
@@ -81,6 +92,11 @@ class Hip:
         if rc != 0:
             raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
         return float(ms.value)
+
+
+def _hip_ok(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with HIP error {rc}")
 
 
 def synthetic(seed, layers, kv_heads, query_heads, seq_len, head_dim, std):
@@ -210,21 +226,30 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
     lib = _lib.load()
     rot = _lib.TQ_ROTATE_KEYS | _lib.TQ_ROTATE_VALUES
     dflags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT
-    calls = []  # per step: list of (fn, args) for every layer
+    # Per step and layer: tq_decode_append (pack the new token and decode with it, one launch) -- the
+    # default -- or the two-launch tq_append + tq_decode sequence it replaces (`unfused`).
+    calls, calls_unfused = [], []
     for t in range(steps):
         seq = s0 + t
-        step_calls = []
+        fused_step, unfused_step = [], []
         for l, st in enumerate(stores):
-            step_calls.append((lib.tq_append, (
+            fused_step.append((lib.tq_decode_append, (
+                queries[t, l].data_ptr(), new_k[t, l].data_ptr(), new_v[t, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d,
+                bits, st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, seq,
+                st.key_centroids.data_ptr(), st.value_centroids.data_ptr(), st.key_boundaries.data_ptr(),
+                st.value_boundaries.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), rot, dflags, 0,
+                ws.data_ptr(), out[l].data_ptr(), stream)))
+            unfused_step.append((lib.tq_append, (
                 new_k[t, l].data_ptr(), new_v[t, l].data_ptr(), _lib.TQ_F16, 1, hkv, 1, d, bits, st.signs_left.data_ptr(),
                 st.signs_right.data_ptr(), rot, st.key_boundaries.data_ptr(), st.value_boundaries.data_ptr(),
                 st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, seq, stream)))
-            step_calls.append((lib.tq_decode, (
+            unfused_step.append((lib.tq_decode, (
                 queries[t, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d, bits, st.key_codes.data_ptr(),
                 st.value_codes.data_ptr(), st.capacity, seq + 1, st.key_centroids.data_ptr(),
                 st.value_centroids.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), dflags, None, None,
                 0, ws.data_ptr(), out[l].data_ptr(), stream)))
-        calls.append(step_calls)
+        calls.append(fused_step)
+        calls_unfused.append(unfused_step)
 
     # warm-up: decode-only passes over every layer at the prefill length (the caches are not changed)
     for _ in range(args.warmup):
@@ -237,29 +262,80 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
     # a 1 GiB read between steps evicts the slabs from the 256 MB Infinity Cache; it is outside the events
     flush = torch.empty(2**30, dtype=torch.uint8, device=dev)
     sink = torch.empty(8 * 1024, dtype=torch.float32, device=dev)
-    events = [(hip.event(), hip.event()) for _ in range(steps)]
-    torch.cuda.synchronize()
     hip.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-    t_start = time.perf_counter()
-    for t in range(steps):
-        _lib.check(lib.tq_stream_read(flush.data_ptr(), 2**30, sink.data_ptr(), 0, stream, None, None))
-        hip.lib.hipEventRecord(events[t][0], stream)
+
+    def timed_steps(stream_handle, launch_step):
+        events = [(hip.event(), hip.event()) for _ in range(steps)]
+        torch.cuda.synchronize()
+        t_start = time.perf_counter()
+        for t in range(steps):
+            _lib.check(lib.tq_stream_read(flush.data_ptr(), 2**30, sink.data_ptr(), 0, stream_handle, None, None))
+            hip.lib.hipEventRecord(events[t][0], stream_handle)
+            launch_step(t)
+            hip.lib.hipEventRecord(events[t][1], stream_handle)
+        hip.lib.hipStreamSynchronize(ctypes.c_void_p(stream_handle))
+        torch.cuda.synchronize()
+        host = (time.perf_counter() - t_start) / steps
+        return np.array([hip.elapsed_ms(a, b) for a, b in events]) * 1e3, host
+
+    def eager_step(t):
         for fn, a in calls[t]:
             rc = fn(*a)
             if rc != 0:
                 _lib.check(rc)
-        hip.lib.hipEventRecord(events[t][1], stream)
-    torch.cuda.synchronize()
-    host_s = time.perf_counter() - t_start
-    step_us = np.array([hip.elapsed_ms(a, b) for a, b in events]) * 1e3
+
+    # The unfused sequence first; every variant replays the same steps (a step rewrites the same token at
+    # the same row), so each starts from the same cache contents.
+    unfused_us, _ = timed_steps(stream, lambda t: [_lib.check(fn(*a)) for fn, a in calls_unfused[t]])
+    unfused_out = out.clone()
+    step_us, host_s = timed_steps(stream, eager_step)
+    eager_out = out.clone()
+    fused_dev = float(np.max(np.abs(eager_out.cpu().numpy() - unfused_out.cpu().numpy())))
+
+    # The same steps captured as one HIP graph per step (the appended offset and the sequence length change
+    # every step) and replayed once each: the device-side step latency without host launch overhead.
+    # Replaying a step is idempotent (the same token is written at the same offset).
+    hl = hip.lib
+    gstream = ctypes.c_void_p()
+    _hip_ok(hl.hipStreamCreate(ctypes.byref(gstream)), "hipStreamCreate")
+    graph_calls = []
+    for t in range(steps):
+        step_calls = []
+        for fn, a in calls[t]:
+            a = list(a)
+            a[-1] = gstream.value
+            step_calls.append((fn, tuple(a)))
+        graph_calls.append(step_calls)
+    execs = []
+    for t in range(steps):
+        _hip_ok(hl.hipStreamBeginCapture(gstream, 2), "hipStreamBeginCapture")
+        for fn, a in graph_calls[t]:
+            rc = fn(*a)
+            if rc != 0:
+                _lib.check(rc)
+        graph = ctypes.c_void_p()
+        _hip_ok(hl.hipStreamEndCapture(gstream, ctypes.byref(graph)), "hipStreamEndCapture")
+        exe = ctypes.c_void_p()
+        _hip_ok(hl.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)), "hipGraphInstantiate")
+        _hip_ok(hl.hipGraphDestroy(graph), "hipGraphDestroy")
+        execs.append(exe)
+    graph_us, graph_host = timed_steps(gstream.value, lambda t: _hip_ok(hl.hipGraphLaunch(execs[t], gstream),
+                                                                      "hipGraphLaunch"))
+    graph_dev = float(np.max(np.abs(out.cpu().numpy() - eager_out.cpu().numpy())))
+    for exe in execs:
+        hl.hipGraphExecDestroy(exe)
+    hl.hipStreamDestroy(gstream)
     packed = [L * hkv * (s0 + t + 1) * 2 * w * 4 for t in range(steps)]
     total_bytes = float(sum(packed))
-    mean_us = float(step_us.mean())
-    log(f"step mean {mean_us:.1f} us (median {np.median(step_us):.1f}); host enqueue {host_s / steps * 1e6:.1f} us/step")
+    mean_us = float(graph_us.mean())
+    log(f"graph-replayed step mean {mean_us:.1f} us (median {np.median(graph_us):.1f}); eager step mean "
+        f"{step_us.mean():.1f} us with host enqueue {host_s * 1e6:.1f} us/step; graph vs eager output max diff {graph_dev:.1e}")
+    log(f"unfused (tq_append + tq_decode) eager step mean {unfused_us.mean():.1f} us; fused vs unfused output max "
+        f"diff {fused_dev:.1e}")
 
     result = {
         "metric": f"decode-loop step latency and packed KV GB/s ({args.workload})",
-        "value": round(total_bytes / (step_us.sum() * 1e-6) / 1e9, 2),
+        "value": round(total_bytes / (graph_us.sum() * 1e-6) / 1e9, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
@@ -280,12 +356,24 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
             "prefill": s0,
             "query_dtype": "f16",
             "n_splits_at_prefill": n_splits[0],
-            "step": "per layer: tq_append (1 token) + tq_decode (split kernel + merge kernel)",
+            "step": "per layer: tq_decode_append (pack the new token and decode with it) + merge kernel",
         },
         "step_us_mean": round(mean_us, 2),
-        "step_us_median": round(float(np.median(step_us)), 2),
-        "step_us_min": round(float(step_us.min()), 2),
-        "host_enqueue_us_per_step": round(host_s / steps * 1e6, 1),
+        "step_us_median": round(float(np.median(graph_us)), 2),
+        "step_us_min": round(float(graph_us.min()), 2),
+        "timing": "per step: events around one HIP graph replay (all layers' appends and decodes), 1 GiB read "
+        "between steps outside the events",
+        "eager": {
+            "step_us_mean": round(float(step_us.mean()), 2),
+            "host_enqueue_us_per_step": round(host_s * 1e6, 1),
+            "note": "host-driven launches through ctypes; slower than the device when the enqueue time exceeds it",
+        },
+        "graph_vs_eager_max_abs": graph_dev,
+        "unfused": {
+            "step_us_mean": round(float(unfused_us.mean()), 2),
+            "step": "per layer: tq_append + tq_decode (two launches plus the merge)",
+            "fused_vs_unfused_max_abs": fused_dev,
+        },
         "packed_bytes_last_step": packed[-1],
     }
     if not args.no_cpu_baseline:

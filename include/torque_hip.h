@@ -115,6 +115,25 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
               const float* signs_left, const float* signs_right, int flags, const float* current_keys,
               const float* current_values, int n_splits, void* workspace, float* out, hipStream_t stream);
 
+/* Append one token to the packed slabs and decode with it in one launch:
+ * the same as tq_append(new token at row seq_len) followed by
+ * tq_decode(seq_len + 1) -- the packed words are identical and the output
+ * matches to float rounding -- but the new token's codes are produced inside
+ * the decode's split-0 workgroups and the token joins the softmax from
+ * registers, saving the append launch of every decode step.  new_keys /
+ * new_values are [L, Hkv, D] in `dtype` (also the query dtype); append_flags
+ * TQ_ROTATE_KEYS / TQ_ROTATE_VALUES as for tq_append, decode_flags as for
+ * tq_decode.  seq_len (tokens already in the slabs) must be below capacity.
+ * Replaces the per-layer decode_mlx_with_current + append pair of the
+ * reference's Qwen decode step (qwen_mlx.py:826-828; cache_mlx.py:236-302,
+ * 151-171). */
+int tq_decode_append(const void* query, const void* new_keys, const void* new_values, int dtype, int num_layers,
+                     int query_heads, int kv_heads, int head_dim, int bits, uint32_t* key_codes,
+                     uint32_t* value_codes, int64_t capacity, int64_t seq_len, const float* key_centroids,
+                     const float* value_centroids, const float* key_boundaries, const float* value_boundaries,
+                     const float* signs_left, const float* signs_right, int append_flags, int decode_flags,
+                     int n_splits, void* workspace, float* out, hipStream_t stream);
+
 /* Same as tq_decode; start/stop events (may be NULL) are bound to the split
  * kernel itself, so hipEventElapsedTime gives its execution time (the merge
  * kernel, when launched, follows it on the stream). */

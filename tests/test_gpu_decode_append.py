@@ -1,0 +1,133 @@
+"""tq_decode_append: one launch that packs the new token and decodes with it.
+
+Checked against the two-launch sequence it replaces (append, then decode over
+the grown cache): the packed words must be identical and the outputs equal to
+float rounding; and against the oracle's append-then-decode.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import torque_oracle as o
+
+pytestmark = pytest.mark.gpu
+
+
+def _pair(bits, head_dim, layers, kv_heads, capacity, fused=False, strategy="split_batched"):
+    import torque_hip as th
+
+    cfg = th.TorqueConfig(bit_width=bits, head_dim=head_dim, num_layers=layers, kv_heads=kv_heads, fused_weights=fused)
+    kw = dict(config=cfg, initial_capacity=capacity, decode_tail_capacity=0, decode_strategy=strategy)
+    return th.TorqueKVCacheHIP(**kw), th.TorqueKVCacheHIP(**kw)
+
+
+def _codes(cache):
+    s = cache.sequence_length
+    return tuple(t[:, :, :s].cpu().numpy() for t in (cache._key_codes, cache._value_codes))
+
+
+@pytest.mark.parametrize(
+    "bits,head_dim,layers,kv_heads,group,prefill",
+    [
+        (4, 128, 1, 2, 4, 0),
+        (4, 128, 2, 2, 4, 37),
+        (3, 64, 1, 4, 4, 300),
+        (2, 256, 1, 2, 2, 513),
+        (4, 256, 1, 1, 1, 5),
+        (4, 64, 1, 2, 8, 2100),
+        (3, 128, 1, 3, 3, 1000),
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_decode_append_matches_append_then_decode(hip_device, bits, head_dim, layers, kv_heads, group, prefill, dtype):
+    gen = torch.Generator(device=hip_device).manual_seed(bits * 1000 + head_dim + prefill)
+    a, b = _pair(bits, head_dim, layers, kv_heads, capacity=64)
+    hq = kv_heads * group
+    if prefill:
+        k = torch.randn((layers, kv_heads, prefill, head_dim), generator=gen, device=hip_device).to(dtype)
+        v = torch.randn((layers, kv_heads, prefill, head_dim), generator=gen, device=hip_device).to(dtype)
+        a.append_many(key=k, value=v)
+        b.append_many(key=k, value=v)
+    for step in range(3):
+        q = torch.randn((layers, hq, head_dim), generator=gen, device=hip_device).to(dtype)
+        k = torch.randn((layers, kv_heads, head_dim), generator=gen, device=hip_device).to(dtype)
+        v = torch.randn((layers, kv_heads, head_dim), generator=gen, device=hip_device).to(dtype)
+        got = a.decode_append(query=q, key=k, value=v, return_numpy=False).cpu().numpy()
+        b.append(key=k, value=v)
+        exp = b.decode(query=q, return_numpy=False).cpu().numpy()
+        assert a.sequence_length == b.sequence_length == prefill + step + 1
+        for x, y in zip(_codes(a), _codes(b)):
+            np.testing.assert_array_equal(x, y)
+        np.testing.assert_allclose(got, exp, atol=2e-6, rtol=1e-5, err_msg=f"step {step}")
+
+
+def test_decode_append_against_oracle_and_split_counts(hip_device):
+    import torque_hip as th
+
+    rng = np.random.default_rng(5)
+    cfg = th.TorqueConfig(bit_width=4, head_dim=128, num_layers=1, kv_heads=2)
+    cache = th.TorqueKVCacheHIP(config=cfg, initial_capacity=4096, decode_tail_capacity=0)
+    k0 = rng.normal(size=(1, 2, 3000, 128)).astype(np.float32)
+    v0 = rng.normal(size=(1, 2, 3000, 128)).astype(np.float32)
+    cache.append_many(key=k0, value=v0)
+    q = rng.normal(size=(8, 128)).astype(np.float32)
+    kn = rng.normal(size=(2, 128)).astype(np.float32)
+    vn = rng.normal(size=(2, 128)).astype(np.float32)
+    st = cache._store
+    outs = []
+    for ns in (1, 5, 64):
+        st.length = 3000  # rewrite the same token at the same row each time
+        outs.append(
+            st.decode_append(torch.from_numpy(q).to(hip_device).reshape(1, 8, 128),
+                             torch.from_numpy(kn).to(hip_device).reshape(1, 2, 1, 128),
+                             torch.from_numpy(vn).to(hip_device).reshape(1, 2, 1, 128),
+                             rotate_query=True, inverse_output=True, rotate_keys=True, rotate_values=True,
+                             n_splits=ns).cpu().numpy()[0]
+        )
+    model = o.OracleCache(bit_width=4, head_dim=128, num_layers=1, kv_heads=2,
+                          key_centroids=cache.key_codebook.centroids, value_centroids=cache.value_codebook.centroids,
+                          signs_left=cache.rotation.signs_left, signs_right=cache.rotation.signs_right)
+    model.append(np.concatenate([k0, kn.reshape(1, 2, 1, 128)], axis=2), np.concatenate([v0, vn.reshape(1, 2, 1, 128)], axis=2))
+    exp = model.decode(q.reshape(1, 8, 128))[0]
+    cache.sequence_length = 3001
+    kc, vc = _codes(cache)
+    np.testing.assert_array_equal(kc.view(np.uint32), model.k_codes)
+    np.testing.assert_array_equal(vc.view(np.uint32), model.v_codes)
+    for ns, out in zip((1, 5, 64), outs):
+        np.testing.assert_allclose(out, exp, atol=2e-6, rtol=1e-5, err_msg=f"n_splits {ns}")
+
+
+def test_decode_append_flags_growth_and_errors(hip_device):
+    from torque_hip import _lib
+
+    rng = np.random.default_rng(9)
+    for fused in (False, True):
+        a, b = _pair(3, 64, 1, 2, capacity=2, fused=fused, strategy="fused_per_head")
+        a.rotate_values_on_append = b.rotate_values_on_append = False
+        for step in range(5):  # grows 2 -> 4 -> 8
+            q = rng.normal(size=(4, 64)).astype(np.float32)
+            k = rng.normal(size=(2, 64)).astype(np.float32)
+            v = rng.normal(size=(2, 64)).astype(np.float32)
+            got = a.decode_append(query=q, key=k, value=v)
+            b.append(key=k, value=v)
+            np.testing.assert_allclose(got, b.decode(query=q), atol=2e-6, rtol=1e-5)
+        assert a.capacity == b.capacity == 8
+        for x, y in zip(_codes(a), _codes(b)):
+            np.testing.assert_array_equal(x, y)
+    with pytest.raises(ValueError, match="single token"):
+        a.decode_append(query=np.zeros((4, 64), np.float32), key=np.zeros((2, 3, 64), np.float32),
+                        value=np.zeros((2, 3, 64), np.float32))
+    st = a._store
+    q = torch.zeros((1, 4, 64), device=hip_device)
+    kv = torch.zeros((1, 2, 1, 64), device=hip_device)
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device=hip_device)
+    out = torch.empty((1, 4, 64), device=hip_device)
+    with pytest.raises(ValueError, match="slab is full"):
+        _lib.call("tq_decode_append", q.data_ptr(), kv.data_ptr(), kv.data_ptr(), _lib.TQ_F32, 1, 4, 2, 64, 3,
+                  st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, st.capacity,
+                  st.key_centroids.data_ptr(), st.value_centroids.data_ptr(), st.key_boundaries.data_ptr(),
+                  st.value_boundaries.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), 3, 3, 0,
+                  ws.data_ptr(), out.data_ptr(), None)

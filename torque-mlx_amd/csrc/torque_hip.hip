@@ -178,6 +178,16 @@ struct DecodeArgs {
   float sqrt_d;
   float q_scale;  // log2(e) / sqrt(D): scores come out in log2 units
   int rotate_query, inverse_output;
+  // Append mode (new_k != null): the token new_k/new_v [L, Hkv, D] (query
+  // dtype) is rotated, quantized and packed into the slabs at row seq_len by
+  // the split-0 workgroups, and joins the softmax as the current token.
+  const void* new_k;
+  const void* new_v;
+  const float* bnd_k;
+  const float* bnd_v;
+  uint32_t* k_slab;
+  uint32_t* v_slab;
+  int rotate_new_k, rotate_new_v;
   const float* cur_k;  // [L, Hkv, D] or null
   const float* cur_v;
   int n_splits;
@@ -271,6 +281,9 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   __shared__ float s_red[kWavesPerBlock][HG * D];
   __shared__ float s_mw[kWavesPerBlock][HG];
   __shared__ float s_lw[kWavesPerBlock][HG];
+  // append mode: the new token's dequantized rotated key / value, and its codes
+  __shared__ float s_cur[2][Fmt::kHasLut ? D : 1];
+  __shared__ uint8_t s_codes[2][Fmt::kHasLut ? D : 1];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
   const int gi = lane / LPT, slice = lane % LPT;
@@ -322,6 +335,23 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       lut_kv[1] = Fmt::lut_entry(tid, a.cent_v);
     }
   }
+  // Append mode: the split-0 workgroups quantize the new token (wavefront 0
+  // the key, 1 the value) while their first K/V rows are in flight.
+  const bool appending = Fmt::kHasLut && a.new_k != nullptr;
+  const bool appender = appending && split == 0 && wave < 2;
+  constexpr int kLevels = Fmt::kHasLut ? (1 << Fmt::kBits) - 1 : 1;
+  float tok[E], bnd[kLevels];
+  if (appender) {
+    const int64_t toff = static_cast<int64_t>(lkv) * D + lane * E;
+    const void* src = wave == 0 ? a.new_k : a.new_v;
+#pragma unroll
+    for (int i = 0; i < E; ++i)
+      tok[i] = QF16 ? __half2float(static_cast<const __half*>(src)[toff + i]) : static_cast<const float*>(src)[toff + i];
+    const float* b = wave == 0 ? a.bnd_k : a.bnd_v;
+#pragma unroll
+    for (int k = 0; k < kLevels; ++k) bnd[k] = b[k];
+  }
+
   // Query bits are loaded raw and converted after the K/V requests below, so
   // the conversion does not hold those requests back.
   // A lane's query values as raw 32-bit words: E floats, or (E + 1) / 2 words
@@ -341,12 +371,12 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < E / 2; ++i) qw[i] = q[i];
     }
-    if (a.rotate_query) {
+  }
+  if ((wave < HG && a.rotate_query) || appender) {
 #pragma unroll
-      for (int i = 0; i < E; ++i) {
-        sg_first[i] = a.signs_right[lane * E + i];
-        sg_second[i] = a.signs_left[lane * E + i];
-      }
+    for (int i = 0; i < E; ++i) {
+      sg_first[i] = a.signs_right[lane * E + i];
+      sg_second[i] = a.signs_left[lane * E + i];
     }
   }
 
@@ -366,6 +396,15 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     }
   }
 
+  // ---- append mode: rotate (as on append) and quantize the new token.
+  if constexpr (Fmt::kHasLut) {
+    if (appender) {
+      if (wave == 1 ? a.rotate_new_v : a.rotate_new_k) wave_rotate_signs<D>(tok, sg_first, sg_second, a.sqrt_d);
+#pragma unroll
+      for (int i = 0; i < E; ++i) s_codes[wave][lane * E + i] = static_cast<uint8_t>(quantize_count<Fmt::kBits>(tok[i], bnd));
+    }
+  }
+
   // ---- queries: optional rotation (bit-identical to the reference), then
   // the softmax scale and log2(e) folded in, so scores are in log2 units.
   if (wave < HG) {
@@ -378,6 +417,19 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     for (int i = 0; i < E; ++i) s_q[wave][lane * E + i] = qe[i] * a.q_scale;
   }
   __syncthreads();
+  if constexpr (Fmt::kHasLut) {
+    if (appender) {
+      // Dequantized values through the centroid table (entry c holds centroid
+      // c first); one head group writes the packed words (all compute them).
+#pragma unroll
+      for (int i = 0; i < E; ++i) s_cur[wave][lane * E + i] = Fmt::first_centroid(s_lut[wave][s_codes[wave][lane * E + i]]);
+      constexpr int W = D * Fmt::kBits / 32;
+      if (hg == 0 && lane < W) {
+        uint32_t* dst = (wave == 0 ? a.k_slab : a.v_slab) + (static_cast<int64_t>(lkv) * a.cap + a.seq_len) * W + lane;
+        *dst = pack_word<Fmt::kBits, D>(s_codes[wave], lane);
+      }
+    }
+  }
 
   // ---- head slots.  With HG == 4 and U == 2 the softmax runs in quad mode
   // (see process): each lane exponentiates only the pairs (token, head) of
@@ -610,9 +662,9 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       float l = s_lw[0][wave];
 #pragma unroll
       for (int w = 1; w < kWavesPerBlock; ++w) l += s_lw[w][wave];
-      const bool cur = a.cur_k != nullptr;
-      finish_row<D>(&s_red[0][wave * D], M[wave], l, s_q[wave], cur ? a.cur_k + static_cast<int64_t>(lkv) * D : nullptr,
-                    cur ? a.cur_v + static_cast<int64_t>(lkv) * D : nullptr, a.inverse_output, a.signs_left,
+      const float* ck = appending ? s_cur[0] : a.cur_k ? a.cur_k + static_cast<int64_t>(lkv) * D : nullptr;
+      const float* cv = appending ? s_cur[1] : a.cur_v ? a.cur_v + static_cast<int64_t>(lkv) * D : nullptr;
+      finish_row<D>(&s_red[0][wave * D], M[wave], l, s_q[wave], ck, cv, a.inverse_output, a.signs_left,
                     a.signs_right, a.sqrt_d, a.out + (qhg0 + wave) * D);
     }
     return;
@@ -644,8 +696,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       a.ws_ml[((qhg0 + wave) * a.n_splits + split) * 2] = M[wave];
       a.ws_ml[((qhg0 + wave) * a.n_splits + split) * 2 + 1] = l;
     }
-    if (split == 0 && a.cur_k != nullptr) {
-      const float* ck = a.cur_k + static_cast<int64_t>(lkv) * D + lane * E;
+    if (split == 0 && (appending || a.cur_k != nullptr)) {
+      const float* ck = (appending ? s_cur[0] : a.cur_k + static_cast<int64_t>(lkv) * D) + lane * E;
       float dot = 0.f;
 #pragma unroll
       for (int i = 0; i < E; ++i) dot = fmaf(s_q[wave][lane * E + i], ck[i], dot);
@@ -653,7 +705,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       if (lane == 0) a.ws_cur_s[qhg0 + wave] = dot;
       if (wave == 0 && hg == 0) {
         float v[E];
-        const float* cv = a.cur_v + static_cast<int64_t>(lkv) * D + lane * E;
+        const float* cv = (appending ? s_cur[1] : a.cur_v + static_cast<int64_t>(lkv) * D) + lane * E;
 #pragma unroll
         for (int i = 0; i < E; ++i) v[i] = cv[i];
         if (a.inverse_output) wave_rotate<D>(v, a.signs_left, a.signs_right, a.sqrt_d);
@@ -867,7 +919,8 @@ struct Plan {
   int64_t split_len;
 };
 
-constexpr int kMinTokensPerSplit = 256;
+constexpr int kMinTokensPerSplit = 128;
+constexpr int kSplitAlign = 32;
 
 int default_splits(int units, int64_t seq_len, int num_cus) {
   if (num_cus <= 0) num_cus = 256;
@@ -906,8 +959,7 @@ WsLayout workspace_layout(int64_t lq, int64_t lkv, int head_dim, int n_splits) {
   return w;
 }
 
-// Fills the split plan; tokens per split are a multiple of 256 rows so every
-// split starts on a whole number of workgroup steps.
+// Fills the split plan; tokens per split are a multiple of kSplitAlign rows.
 int make_plan(int num_layers, int kv_heads, int query_heads, int head_dim, int64_t seq_len, int n_splits, Plan* p) {
   if (num_layers <= 0 || kv_heads <= 0 || query_heads <= 0)
     return fail(TQ_ERR_BAD_ARG, "num_layers, kv_heads and query_heads must be positive");
@@ -922,7 +974,7 @@ int make_plan(int num_layers, int kv_heads, int query_heads, int head_dim, int64
   int ns = n_splits > 0 ? n_splits : default_splits(p->units, seq_len, device_cu_count());
   if (ns > kMaxSplits) return fail(TQ_ERR_BAD_ARG, "n_splits must be at most " + std::to_string(kMaxSplits));
   int64_t len = std::max<int64_t>(1, (seq_len + ns - 1) / ns);
-  len = ((len + 255) / 256) * 256;
+  len = (len + kSplitAlign - 1) / kSplitAlign * kSplitAlign;
   const int64_t eff = std::max<int64_t>(1, (seq_len + len - 1) / len);
   p->n_splits = static_cast<int>(std::min<int64_t>(eff, ns));
   p->split_len = len;
@@ -980,11 +1032,20 @@ int dispatch_d(const DecodeArgs& a, int head_dim, int hg, int nblk, hipStream_t 
 
 // Common front end of tq_decode / tq_decode_dense.  fmt: 2/3/4 packed bits,
 // 16 dense fp16, 32 dense fp32.
+// The new token of tq_decode_append.
+struct AppendSpec {
+  const void* keys;
+  const void* values;
+  const float* key_boundaries;
+  const float* value_boundaries;
+  int flags;  // TQ_ROTATE_KEYS | TQ_ROTATE_VALUES
+};
+
 int decode_common(int fmt, const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
                   int head_dim, const void* keys, const void* values, int64_t capacity, int64_t seq_len,
                   const float* cent_k, const float* cent_v, const float* signs_left, const float* signs_right,
                   int flags, const float* cur_k, const float* cur_v, int n_splits, void* workspace, float* out,
-                  hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+                  hipStream_t stream, hipEvent_t start, hipEvent_t stop, const AppendSpec* app = nullptr) {
   int rc = check_geometry(head_dim, 0);
   if (rc) return rc;
   if (query == nullptr || out == nullptr || workspace == nullptr)
@@ -995,6 +1056,14 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   if (capacity < seq_len) return fail(TQ_ERR_BAD_ARG, "capacity must be >= seq_len");
   if ((cur_k == nullptr) != (cur_v == nullptr))
     return fail(TQ_ERR_BAD_ARG, "current_keys and current_values must both be given or both be null");
+  if (app != nullptr) {
+    if (app->keys == nullptr || app->values == nullptr || app->key_boundaries == nullptr ||
+        app->value_boundaries == nullptr || keys == nullptr || values == nullptr)
+      return fail(TQ_ERR_BAD_ARG, "new keys/values, boundaries and both slabs must be non-null");
+    if (seq_len >= capacity) return fail(TQ_ERR_BAD_ARG, "slab is full: seq_len must be below capacity");
+    if ((app->flags & (TQ_ROTATE_KEYS | TQ_ROTATE_VALUES)) && (signs_left == nullptr || signs_right == nullptr))
+      return fail(TQ_ERR_BAD_ARG, "rotation flags need signs_left and signs_right");
+  }
   if ((flags & (TQ_ROTATE_QUERY | TQ_INVERSE_OUTPUT)) && (signs_left == nullptr || signs_right == nullptr))
     return fail(TQ_ERR_BAD_ARG, "rotation flags need signs_left and signs_right");
   const bool packed = fmt == 2 || fmt == 3 || fmt == 4;
@@ -1034,6 +1103,16 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   a.inverse_output = (flags & TQ_INVERSE_OUTPUT) != 0;
   a.cur_k = cur_k;
   a.cur_v = cur_v;
+  if (app != nullptr) {
+    a.new_k = app->keys;
+    a.new_v = app->values;
+    a.bnd_k = app->key_boundaries;
+    a.bnd_v = app->value_boundaries;
+    a.k_slab = const_cast<uint32_t*>(static_cast<const uint32_t*>(keys));
+    a.v_slab = const_cast<uint32_t*>(static_cast<const uint32_t*>(values));
+    a.rotate_new_k = (app->flags & TQ_ROTATE_KEYS) != 0;
+    a.rotate_new_v = (app->flags & TQ_ROTATE_VALUES) != 0;
+  }
   a.n_splits = p.n_splits;
   a.split_len = p.split_len;
   a.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
@@ -1049,7 +1128,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   m.n_splits = p.n_splits;
   m.ws_ml = a.ws_ml;
   m.ws_acc = a.ws_acc;
-  m.cur_s = cur_k != nullptr ? a.ws_cur_s : nullptr;
+  m.cur_s = (cur_k != nullptr || app != nullptr) ? a.ws_cur_s : nullptr;
   m.cur_v = a.ws_cur_v;
   m.out = out;
 
@@ -1413,6 +1492,20 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
   return tq_decode_timed(query, query_dtype, num_layers, query_heads, kv_heads, head_dim, bits, key_codes,
                          value_codes, capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right,
                          flags, current_keys, current_values, n_splits, workspace, out, stream, nullptr, nullptr);
+}
+
+int tq_decode_append(const void* query, const void* new_keys, const void* new_values, int dtype, int num_layers,
+                     int query_heads, int kv_heads, int head_dim, int bits, uint32_t* key_codes,
+                     uint32_t* value_codes, int64_t capacity, int64_t seq_len, const float* key_centroids,
+                     const float* value_centroids, const float* key_boundaries, const float* value_boundaries,
+                     const float* signs_left, const float* signs_right, int append_flags, int decode_flags,
+                     int n_splits, void* workspace, float* out, hipStream_t stream) {
+  int rc = check_geometry(head_dim, bits);
+  if (rc) return rc;
+  const AppendSpec app{new_keys, new_values, key_boundaries, value_boundaries, append_flags};
+  return decode_common(bits, query, dtype, num_layers, query_heads, kv_heads, head_dim, key_codes, value_codes,
+                       capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, decode_flags,
+                       nullptr, nullptr, n_splits, workspace, out, stream, nullptr, nullptr, &app);
 }
 
 int tq_decode_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,

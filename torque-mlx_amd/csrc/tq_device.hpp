@@ -272,6 +272,7 @@ struct PackedB4 {
     return D * kBits / 8;
   }
   __device__ static LutT lut_entry(int e, const float* __restrict__ c) { return make_float2(c[e & 15], c[e >> 4]); }
+  __device__ static float first_centroid(const LutT& t) { return t.x; }
   __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
     const uint2 v = *reinterpret_cast<const uint2*>(row + 8 * slice);
     return {v.x, v.y};
@@ -305,6 +306,7 @@ struct PackedB2 {
   __device__ static LutT lut_entry(int e, const float* __restrict__ c) {
     return make_float4(c[e & 3], c[(e >> 2) & 3], c[(e >> 4) & 3], c[(e >> 6) & 3]);
   }
+  __device__ static float first_centroid(const LutT& t) { return t.x; }
   __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
     return {*reinterpret_cast<const uint32_t*>(row + 4 * slice)};
   }
@@ -337,6 +339,7 @@ struct PackedB3 {
     return D * kBits / 8;
   }
   __device__ static LutT lut_entry(int e, const float* __restrict__ c) { return make_float2(c[e & 7], c[e >> 3]); }
+  __device__ static float first_centroid(const LutT& t) { return t.x; }
   __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
     const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + ((3 * slice) >> 1);
     return {w[0], w[1]};
@@ -354,6 +357,7 @@ struct PackedB3 {
 
 // Dense float16 rows: 8 dims = 16 bytes per slice.
 struct DenseF16 {
+  static constexpr int kBits = 0;  // not a packed format
   static constexpr int kSliceDims = 8;
   static constexpr bool kHasLut = false;
   static constexpr int kLutEntries = 1;
@@ -366,6 +370,7 @@ struct DenseF16 {
     return D * 2;
   }
   __device__ static LutT lut_entry(int, const float*) { return 0.f; }
+  __device__ static float first_centroid(const LutT& t) { return t; }
   __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
     return {*reinterpret_cast<const uint4*>(row + 16 * slice)};
   }
@@ -381,6 +386,7 @@ struct DenseF16 {
 
 // Dense float32 rows: 4 dims = 16 bytes per slice.
 struct DenseF32 {
+  static constexpr int kBits = 0;  // not a packed format
   static constexpr int kSliceDims = 4;
   static constexpr bool kHasLut = false;
   static constexpr int kLutEntries = 1;
@@ -393,6 +399,7 @@ struct DenseF32 {
     return D * 4;
   }
   __device__ static LutT lut_entry(int, const float*) { return 0.f; }
+  __device__ static float first_centroid(const LutT& t) { return t; }
   __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
     return {*reinterpret_cast<const float4*>(row + 16 * slice)};
   }

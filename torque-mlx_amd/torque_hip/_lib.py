@@ -57,6 +57,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i,
         [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _p, _p, _p],
     ),
+    "tq_decode_append": (
+        _i,
+        [_p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p],
+    ),
     "tq_decode_dense": (_i, [_p, _i, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _p, _p, _i, _i, _p, _p, _p]),
     "tq_decode_dense_timed": (
         _i,

@@ -15,7 +15,7 @@ import torch
 from torque_hip import _lib
 from torque_hip._tensors import dtype_code, stream_handle
 from torque_hip.config import TorqueConfig
-from torque_hip.ops import packed_decode
+from torque_hip.ops import packed_decode, packed_decode_append
 from torque_hip.quantization import Codebook, codebook_boundaries
 from torque_hip.rotation import RotationSpec
 
@@ -167,6 +167,52 @@ class SlabStore:
             current_values=None if current is None else current[1],
             n_splits=n_splits,
         )
+
+    def decode_append(
+        self,
+        queries: torch.Tensor,
+        keys: torch.Tensor,
+        values: torch.Tensor,
+        *,
+        rotate_query: bool,
+        inverse_output: bool,
+        rotate_keys: bool,
+        rotate_values: bool,
+        n_splits: int | None = None,
+    ) -> torch.Tensor:
+        """Append one token (keys/values [L, Hkv, 1, D]) and decode with it: one launch."""
+        cfg = self.config
+        self.ensure_capacity(self.length + 1)
+        dtype = queries.dtype
+        keys = keys.to(dtype).contiguous()
+        values = values.to(dtype).contiguous()
+        out = packed_decode_append(
+            queries,
+            keys,
+            values,
+            num_layers=cfg.num_layers,
+            query_heads=int(queries.shape[1]),
+            kv_heads=cfg.kv_heads,
+            head_dim=cfg.head_dim,
+            bit_width=cfg.bit_width,
+            key_codes=self.key_codes,
+            value_codes=self.value_codes,
+            capacity=self.capacity,
+            seq_len=self.length,
+            key_centroids=self.key_centroids,
+            value_centroids=self.value_centroids,
+            key_boundaries=self.key_boundaries,
+            value_boundaries=self.value_boundaries,
+            signs_left=self.signs_left,
+            signs_right=self.signs_right,
+            rotate_keys=rotate_keys,
+            rotate_values=rotate_values,
+            rotate_query=rotate_query,
+            inverse_output=inverse_output,
+            n_splits=n_splits,
+        )
+        self.length += 1
+        return out
 
     def export_dequantized(self) -> tuple[torch.Tensor, torch.Tensor]:
         """Dequantized rotated contents [L, Hkv, S, D] (float32, device)."""

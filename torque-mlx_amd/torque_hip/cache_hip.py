@@ -189,6 +189,36 @@ class TorqueKVCacheHIP:
 
     decode_mlx_with_current = decode_with_current
 
+    def decode_append(self, *, query: Any, key: Any, value: Any, return_numpy: bool = True) -> Any:
+        """``decode_with_current`` followed by ``append`` of the same token, in one kernel launch.
+
+        The reference's Qwen decode step makes exactly this pair of calls per layer
+        (qwen_mlx.py:826-828).  The packed words written are identical to ``append``'s and the output
+        matches ``decode_with_current``'s to float rounding; the cache grows by one token.
+        """
+        self.last_decode_profile = {}
+        queries = self._normalize_query_heads(query, "query")
+        keys = self._normalize_layer_heads_sequence(key, "key")
+        values = self._normalize_layer_heads_sequence(value, "value")
+        if int(keys.shape[2]) != 1 or int(values.shape[2]) != 1:
+            raise ValueError("decode_append expects a single token for key/value")
+        query_heads = int(queries.shape[1])
+        self._check_groups(query_heads)
+        profile = self.last_decode_profile if self.profile_decode_components else None
+        with EventTimer(profile, "packed_decode_seconds", self._store.device):
+            outputs = self._store.decode_append(
+                queries,
+                keys,
+                values,
+                rotate_query=self.rotate_queries_on_decode,
+                inverse_output=not self.config.fused_weights,
+                rotate_keys=self.rotate_keys_on_append,
+                rotate_values=self.rotate_values_on_append,
+                n_splits=self._n_splits(),
+            )
+        self.sequence_length += 1
+        return self._finalize_output(outputs, query_heads=query_heads, return_numpy=return_numpy)
+
     def resolve_decode_strategy(self, *, sequence_length: int | None = None) -> str:
         if self.decode_strategy != "auto":
             return self.decode_strategy

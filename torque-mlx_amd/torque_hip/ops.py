@@ -136,6 +136,74 @@ def packed_decode(
     return out
 
 
+def packed_decode_append(
+    query: torch.Tensor,
+    new_keys: torch.Tensor,
+    new_values: torch.Tensor,
+    *,
+    num_layers: int,
+    query_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    bit_width: int,
+    key_codes: torch.Tensor,
+    value_codes: torch.Tensor,
+    capacity: int,
+    seq_len: int,
+    key_centroids: torch.Tensor,
+    value_centroids: torch.Tensor,
+    key_boundaries: torch.Tensor,
+    value_boundaries: torch.Tensor,
+    signs_left: torch.Tensor,
+    signs_right: torch.Tensor,
+    rotate_keys: bool = True,
+    rotate_values: bool = True,
+    rotate_query: bool = False,
+    inverse_output: bool = False,
+    n_splits: int | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One ``tq_decode_append`` launch: pack the new token [L, Hkv, D] into the slabs at row ``seq_len`` and
+    decode over the ``seq_len + 1`` tokens; query, new_keys and new_values share one dtype."""
+    dev = query.device
+    if n_splits is None or n_splits <= 0:
+        n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev)
+    ws = workspace_for(num_layers, kv_heads, query_heads, head_dim, n_splits, dev)
+    if out is None:
+        out = torch.empty((num_layers, query_heads, head_dim), dtype=torch.float32, device=dev)
+    append_flags = (_lib.TQ_ROTATE_KEYS if rotate_keys else 0) | (_lib.TQ_ROTATE_VALUES if rotate_values else 0)
+    decode_flags = (_lib.TQ_ROTATE_QUERY if rotate_query else 0) | (_lib.TQ_INVERSE_OUTPUT if inverse_output else 0)
+    _lib.call(
+        "tq_decode_append",
+        query.data_ptr(),
+        new_keys.data_ptr(),
+        new_values.data_ptr(),
+        dtype_code(query),
+        num_layers,
+        query_heads,
+        kv_heads,
+        head_dim,
+        bit_width,
+        key_codes.data_ptr(),
+        value_codes.data_ptr(),
+        capacity,
+        seq_len,
+        key_centroids.data_ptr(),
+        value_centroids.data_ptr(),
+        key_boundaries.data_ptr(),
+        value_boundaries.data_ptr(),
+        signs_left.data_ptr(),
+        signs_right.data_ptr(),
+        append_flags,
+        decode_flags,
+        n_splits,
+        ws.data_ptr(),
+        out.data_ptr(),
+        stream_handle(dev),
+    )
+    return out
+
+
 def dense_decode(
     query: torch.Tensor,
     keys: torch.Tensor,
