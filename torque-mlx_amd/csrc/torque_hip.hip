@@ -432,32 +432,34 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   }
 
   // ---- head slots.  With HG == 4 and U == 2 the softmax runs in quad mode
-  // (see process): each lane exponentiates only the pairs (token, head) of
-  // its quad position, and the lanes of every odd quad keep their per-head
-  // registers (query slice, accumulators, running maxima) in the order
-  // h ^ 3.  The row_half_mirror / row_mirror exchanges pair quad position p
-  // with position 3 - p of a neighbouring quad, so with that order a lane
-  // always meets the partner that holds the same head.  slot s of a lane
-  // holds head s ^ slot_x.
+  // (see process): the lane at quad position q4 owns head q4 ^ slot_x -- it
+  // sums that head's score, exponentiates it and keeps its softmax sum -- and
+  // its per-head registers (query slice, accumulators, running maxima) hold,
+  // in slot r, head ((q4 + r) & 3) ^ slot_x.  With that rotation the lane
+  // that owns a head is reached by one fixed quad_perm rotation per slot, so
+  // the quad reduction and the weight broadcast need no selects; slot_x = 3
+  // in the odd quads of a token's lanes makes the row_half_mirror / row_mirror
+  // partners (quad position p <-> 3 - p) own the same head.  Other modes use
+  // slot r = head r.
   constexpr bool kQuad = HG == 4 && U == 2;
   const int q4 = lane & 3;
   const int slot_x = (kQuad && LPT >= 8 && ((lane >> 2) & 1)) ? 3 : 0;
+  auto head_of = [&](int r) { return kQuad ? (((q4 + r) & 3) ^ slot_x) : r; };
 
   float qv[HG][SD];
 #pragma unroll
-  for (int s = 0; s < HG; ++s)
+  for (int r = 0; r < HG; ++r)
 #pragma unroll
-    for (int i = 0; i < SD; ++i) qv[s][i] = s_q[s ^ slot_x][slice * SD + i];
+    for (int i = 0; i < SD; ++i) qv[r][i] = s_q[head_of(r)][slice * SD + i];
 
   float m[HG], lsum[HG], acc[HG][SD];
 #pragma unroll
-  for (int s = 0; s < HG; ++s) {
-    m[s] = -INFINITY;
-    lsum[s] = 0.f;  // quad mode uses lsum[0] for the lane's own slot q4
+  for (int r = 0; r < HG; ++r) {
+    m[r] = -INFINITY;
+    lsum[r] = 0.f;  // quad mode uses lsum[0] for the lane's own head
 #pragma unroll
-    for (int i = 0; i < SD; ++i) acc[s][i] = 0.f;
+    for (int i = 0; i < SD; ++i) acc[r][i] = 0.f;
   }
-  float m_own = -INFINITY;  // quad mode: m[q4]
 
   const typename Fmt::LutT* lut_k = s_lut[0];
   const typename Fmt::LutT* lut_v = s_lut[1];
@@ -494,56 +496,51 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) Fmt::decode(vr[u], slice, lut_v, xv[u]);
     if constexpr (kQuad) {
-      // Reduce-scatter inside the quad (DPP xor 2, then xor 1): quad
-      // position q4 ends with the quad's sum for slot q4 of both tokens; the
-      // other quads of the group are added after.  Then each lane
-      // exponentiates its two pairs and the value update takes every pair's
-      // weight from the quad lane that owns it (quad_perm broadcast).
+      // Quad reduction: slot r of the lane r positions back holds this
+      // lane's own head, so three rotations add the quad's partials; the
+      // other quads of the group are added after.  Each lane then
+      // exponentiates its head for both tokens, and the value update takes
+      // the weight of slot r from the lane r positions ahead.
       float own[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const bool hi = (q4 & 2) != 0;
-        const float r0 = (hi ? part[u][2] : part[u][0]) + dpp_move<kDppXor2>(hi ? part[u][0] : part[u][2]);
-        const float r1 = (hi ? part[u][3] : part[u][1]) + dpp_move<kDppXor2>(hi ? part[u][1] : part[u][3]);
-        const bool odd = (q4 & 1) != 0;
-        own[u] = cross_quad_sum<LPT>((odd ? r1 : r0) + dpp_move<kDppXor1>(odd ? r0 : r1));
-      }
+      for (int u = 0; u < U; ++u)
+        own[u] = cross_quad_sum<LPT>(part[u][0] + quad_rotate_from<1>(part[u][1]) + quad_rotate_from<2>(part[u][2]) +
+                                     quad_rotate_from<3>(part[u][3]));
       bool need = false;
 #pragma unroll
-      for (int u = 0; u < U; ++u) need = need || (valid[u] && own[u] > m_own + kRescaleThreshold);
+      for (int u = 0; u < U; ++u) need = need || (valid[u] && own[u] > m[0] + kRescaleThreshold);
       if (__builtin_amdgcn_ballot_w64(need) != 0) {
         // Some running maximum moves (first iteration, rare afterwards).
 #pragma unroll
-        for (int s = 0; s < HG; ++s) {
+        for (int r = 0; r < HG; ++r) {
           float mx = -INFINITY;
 #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const float v = quad_broadcast(own[u], s);
+            const float v = quad_rotate_to(own[u], r);
             mx = valid[u] ? fmaxf(mx, v) : mx;
           }
-          if (mx > m[s] + kRescaleThreshold) {
-            const float alpha = fast_exp2(m[s] - mx);
+          if (mx > m[r] + kRescaleThreshold) {
+            const float alpha = fast_exp2(m[r] - mx);
 #pragma unroll
-            for (int k = 0; k < SD; ++k) acc[s][k] *= alpha;
-            if (q4 == s) lsum[0] *= alpha;
-            m[s] = mx;
+            for (int k = 0; k < SD; ++k) acc[r][k] *= alpha;
+            if (r == 0) lsum[0] *= alpha;
+            m[r] = mx;
           }
         }
-        m_own = q4 == 0 ? m[0] : q4 == 1 ? m[1] : q4 == 2 ? m[2] : m[3];
       }
       float p_own[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        p_own[u] = valid[u] ? fast_exp2(own[u] - m_own) : 0.f;
+        p_own[u] = valid[u] ? fast_exp2(own[u] - m[0]) : 0.f;
         lsum[0] += p_own[u];
       }
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int s = 0; s < HG; ++s) {
-          const float p = quad_broadcast(p_own[u], s);
+        for (int r = 0; r < HG; ++r) {
+          const float p = quad_rotate_to(p_own[u], r);
 #pragma unroll
-          for (int k = 0; k < SD; ++k) acc[s][k] = fmaf(p, xv[u][k], acc[s][k]);
+          for (int k = 0; k < SD; ++k) acc[r][k] = fmaf(p, xv[u][k], acc[r][k]);
         }
     } else {
       // Every lane of the group reduces and exponentiates every pair.
@@ -595,36 +592,37 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   }
 
   // ---- combine the lane groups of this workgroup (log-sum-exp).
-  // Softmax sums per slot: in quad mode each quad position holds its own
-  // slot's sum.  m and these sums are equal on the lanes of a group that
-  // share slot_x, and lanes that share a slice share slot_x, so reducing over
-  // the lanes of one slice covers every group once.  Lane 0 has slot_x = 0.
+  // Softmax sums per slot: in quad mode a lane holds only its own head's sum
+  // (slot 0) and takes slot r's from the lane r positions ahead.  m and these
+  // sums are equal on the lanes of a group that hold the same head in the same
+  // slot, which the lanes sharing a slice do, so reducing over the lanes of
+  // one slice covers every group once.  Lane 0 holds head r in slot r.
   float ls[HG];
 #pragma unroll
-  for (int s = 0; s < HG; ++s) {
+  for (int r = 0; r < HG; ++r) {
     if constexpr (kQuad)
-      ls[s] = group_sum<4>(q4 == s ? lsum[0] : 0.f);
+      ls[r] = r == 0 ? lsum[0] : quad_rotate_to(lsum[0], r);
     else
-      ls[s] = lsum[s];
+      ls[r] = lsum[r];
   }
 #pragma unroll
-  for (int s = 0; s < HG; ++s) {
-    const float mw = strided_reduce<LPT, OpMax>(m[s]);
-    if (lane == 0) s_mw[wave][s] = mw;
+  for (int r = 0; r < HG; ++r) {
+    const float mw = strided_reduce<LPT, OpMax>(m[r]);
+    if (lane == 0) s_mw[wave][r] = mw;
   }
   __syncthreads();
   float buf[NV];
 #pragma unroll
-  for (int s = 0; s < HG; ++s) {
-    const int h = s ^ slot_x;
+  for (int r = 0; r < HG; ++r) {
+    const int h = head_of(r);
     float M = s_mw[0][h];
 #pragma unroll
     for (int w = 1; w < kWavesPerBlock; ++w) M = fmaxf(M, s_mw[w][h]);
-    const float f = ls[s] > 0.f ? fast_exp2(m[s] - M) : 0.f;
-    const float lw = strided_reduce<LPT, OpSum>(ls[s] * f);
-    if (lane == 0) s_lw[wave][s] = lw;
+    const float f = ls[r] > 0.f ? fast_exp2(m[r] - M) : 0.f;
+    const float lw = strided_reduce<LPT, OpSum>(ls[r] * f);
+    if (lane == 0) s_lw[wave][r] = lw;
 #pragma unroll
-    for (int k = 0; k < SD; ++k) buf[s * SD + k] = acc[s][k] * f;
+    for (int k = 0; k < SD; ++k) buf[r * SD + k] = acc[r][k] * f;
   }
   // Reduce-scatter the accumulators over the TPW lane groups of the
   // wavefront: afterwards lane (gi, slice) holds values
@@ -635,8 +633,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < W; ++k) {
       const int v = gi * W + k;
-      const int s = v / SD, d = v - s * SD;
-      s_red[wave][(s ^ slot_x) * D + slice * SD + d] = buf[k];
+      const int r = v / SD, d = v - r * SD;
+      s_red[wave][head_of(r) * D + slice * SD + d] = buf[k];
     }
   }
   __syncthreads();

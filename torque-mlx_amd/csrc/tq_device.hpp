@@ -101,6 +101,31 @@ __device__ __forceinline__ float group_sum(float v) {
   return group_reduce<N, OpSum>(v);
 }
 
+// Quad rotations: every lane of a quad reads the lane R positions back
+// (quad_rotate_from) or ahead (quad_rotate_to), positions taken mod 4.
+template <int R>
+__device__ __forceinline__ float quad_rotate_from(float v) {
+  constexpr int c = ((0 - R) & 3) | (((1 - R) & 3) << 2) | (((2 - R) & 3) << 4) | (((3 - R) & 3) << 6);
+  return dpp_move<c>(v);
+}
+template <int R>
+__device__ __forceinline__ float quad_rotate_to_t(float v) {
+  constexpr int c = (R & 3) | (((1 + R) & 3) << 2) | (((2 + R) & 3) << 4) | (((3 + R) & 3) << 6);
+  return dpp_move<c>(v);
+}
+__device__ __forceinline__ float quad_rotate_to(float v, int r) {
+  switch (r & 3) {
+    case 0:
+      return v;
+    case 1:
+      return quad_rotate_to_t<1>(v);
+    case 2:
+      return quad_rotate_to_t<2>(v);
+    default:
+      return quad_rotate_to_t<3>(v);
+  }
+}
+
 // Value of quad position S, broadcast to every lane of each quad.
 template <int S>
 __device__ __forceinline__ float quad_broadcast_t(float v) {
@@ -146,6 +171,24 @@ __device__ __forceinline__ float strided_reduce(float v) {
   return v;
 }
 
+// The value of lane (lane xor M), M a power of two below 64, moved by DPP
+// inside rows and by the permlane swaps across them.  Exact data movement.
+template <int M>
+__device__ __forceinline__ float xor_partner(float v, int lane) {
+  if constexpr (M == 1) {
+    return dpp_move<kDppXor1>(v);
+  } else if constexpr (M == 2) {
+    return dpp_move<kDppXor2>(v);
+  } else if constexpr (M == 4) {
+    return dpp_move<0x1B>(dpp_move<kDppHalfMirror>(v));  // 7 - i, then quad reversal: i xor 4
+  } else if constexpr (M == 8) {
+    return dpp_move<kDppRor8>(v);
+  } else {
+    const LanePair r = permlane_swap<M>(v, v);
+    return (lane & M) ? r.first : r.second;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Walsh-Hadamard transform of one D-vector held by a wavefront.
 //
@@ -154,6 +197,17 @@ __device__ __forceinline__ float strided_reduce(float v) {
 // (left + right, left - right) with `left` the lower index.  Every element
 // sees the same sequence of IEEE float32 adds/subtracts with the same
 // operands, so the result is bit-identical to the reference.
+// One cross-lane butterfly stage: partners lane and lane xor M.
+template <int M, int E>
+__device__ __forceinline__ void fwht_cross(float (&v)[E], int lane) {
+  const bool upper = (lane & M) != 0;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const float other = xor_partner<M>(v[i], lane);
+    v[i] = upper ? __fsub_rn(other, v[i]) : __fadd_rn(v[i], other);
+  }
+}
+
 template <int D>
 __device__ __forceinline__ void wave_fwht(float (&v)[D / kWave]) {
   constexpr int E = D / kWave;
@@ -169,15 +223,12 @@ __device__ __forceinline__ void wave_fwht(float (&v)[D / kWave]) {
       }
     }
   }
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) {
-    const bool upper = (lane & m) != 0;
-#pragma unroll
-    for (int i = 0; i < E; ++i) {
-      const float other = __shfl_xor(v[i], m);
-      v[i] = upper ? __fsub_rn(other, v[i]) : __fadd_rn(v[i], other);
-    }
-  }
+  fwht_cross<1>(v, lane);
+  fwht_cross<2>(v, lane);
+  fwht_cross<4>(v, lane);
+  fwht_cross<8>(v, lane);
+  fwht_cross<16>(v, lane);
+  fwht_cross<32>(v, lane);
 }
 
 // y = s_second * (H (s_first * x)) / sqrt(D), with the reference's operation
