@@ -313,14 +313,23 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   const uint8_t* kbase = a.k + static_cast<int64_t>(lkv) * a.cap * ROW;
   const uint8_t* vbase = a.v + static_cast<int64_t>(lkv) * a.cap * ROW;
 
-  // Rows past the end of the split are clamped to its last row and masked
-  // out when processed, so loads need no branch.
+  // Iteration i reads through buffer resources over rows
+  // [t0 + i * STRIDE, t1): the workgroup-uniform part of a row's offset sits
+  // in the resource base (scalar arithmetic), the lane's part in a fixed
+  // per-token offset, and rows past the end of the split read as zeros and
+  // are masked out when processed, so loads need no clamp and no branch.
+  int lane_off[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) lane_off[u] = (wave * TPW + u * TPB + gi) * ROW + Fmt::slice_offset(slice);
   auto load_iter = [&](int i, Raw (&kr)[U], Raw (&vr)[U]) {
+    const int64_t row0 = t0 + static_cast<int64_t>(i) * STRIDE;
+    const uint32_t bytes = static_cast<uint32_t>(t1 - row0) * ROW;
+    const BufferRsrc rk = make_rsrc(kbase + row0 * ROW, bytes);
+    const BufferRsrc rv = make_rsrc(vbase + row0 * ROW, bytes);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int t = min(first + i * STRIDE + u * TPB + gi, t1 - 1);
-      kr[u] = Fmt::load(kbase + t * ROW, slice);
-      vr[u] = Fmt::load(vbase + t * ROW, slice);
+      kr[u] = Fmt::load(rk, lane_off[u]);
+      vr[u] = Fmt::load(rv, lane_off[u]);
     }
   };
 
@@ -431,7 +440,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     }
   }
 
-  // ---- head slots.  With HG == 4 and U == 2 the softmax runs in quad mode
+  // ---- head slots.  With HG == 4 the softmax runs in quad mode
   // (see process): the lane at quad position q4 owns head q4 ^ slot_x -- it
   // sums that head's score, exponentiates it and keeps its softmax sum -- and
   // its per-head registers (query slice, accumulators, running maxima) hold,
@@ -441,7 +450,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // in the odd quads of a token's lanes makes the row_half_mirror / row_mirror
   // partners (quad position p <-> 3 - p) own the same head.  Other modes use
   // slot r = head r.
-  constexpr bool kQuad = HG == 4 && U == 2;
+  constexpr bool kQuad = HG == 4;
   const int q4 = lane & 3;
   const int slot_x = (kQuad && LPT >= 8 && ((lane >> 2) & 1)) ? 3 : 0;
   auto head_of = [&](int r) { return kQuad ? (((q4 + r) & 3) ^ slot_x) : r; };
@@ -511,6 +520,9 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       for (int u = 0; u < U; ++u) need = need || (valid[u] && own[u] > m[0] + kRescaleThreshold);
       if (__builtin_amdgcn_ballot_w64(need) != 0) {
         // Some running maximum moves (first iteration, rare afterwards).
+        // The maxima are kept wavefront-wide: slot r holds the same head on
+        // every lane group, and one maximum per head over all the groups'
+        // tokens moves far less often than one per group would.
 #pragma unroll
         for (int r = 0; r < HG; ++r) {
           float mx = -INFINITY;
@@ -519,11 +531,14 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
             const float v = quad_rotate_to(own[u], r);
             mx = valid[u] ? fmaxf(mx, v) : mx;
           }
+          mx = strided_reduce<LPT, OpMax>(mx);
           if (mx > m[r] + kRescaleThreshold) {
-            const float alpha = fast_exp2(m[r] - mx);
+            if (m[r] != -INFINITY) {  // nothing accumulated before the first maximum
+              const float alpha = fast_exp2(m[r] - mx);
 #pragma unroll
-            for (int k = 0; k < SD; ++k) acc[r][k] *= alpha;
-            if (r == 0) lsum[0] *= alpha;
+              for (int k = 0; k < SD; ++k) acc[r][k] *= alpha;
+              if (r == 0) lsum[0] *= alpha;
+            }
             m[r] = mx;
           }
         }
@@ -548,17 +563,29 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int s = 0; s < HG; ++s) part[u][s] = group_sum<LPT>(part[u][s]);
+      // Wavefront-wide running maxima, moved only when some score passes
+      // one by more than the threshold (as in quad mode).
+      bool need = false;
 #pragma unroll
-      for (int s = 0; s < HG; ++s) {
-        float mx = -INFINITY;
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int u = 0; u < U; ++u) mx = valid[u] ? fmaxf(mx, part[u][s]) : mx;
-        if (mx > m[s] + kRescaleThreshold) {
-          const float alpha = fast_exp2(m[s] - mx);
-          lsum[s] *= alpha;
+        for (int s = 0; s < HG; ++s) need = need || (valid[u] && part[u][s] > m[s] + kRescaleThreshold);
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {
 #pragma unroll
-          for (int k = 0; k < SD; ++k) acc[s][k] *= alpha;
-          m[s] = mx;
+        for (int s = 0; s < HG; ++s) {
+          float mx = -INFINITY;
+#pragma unroll
+          for (int u = 0; u < U; ++u) mx = valid[u] ? fmaxf(mx, part[u][s]) : mx;
+          mx = strided_reduce<LPT, OpMax>(mx);
+          if (mx > m[s] + kRescaleThreshold) {
+            if (m[s] != -INFINITY) {  // nothing accumulated before the first maximum
+              const float alpha = fast_exp2(m[s] - mx);
+              lsum[s] *= alpha;
+#pragma unroll
+              for (int k = 0; k < SD; ++k) acc[s][k] *= alpha;
+            }
+            m[s] = mx;
+          }
         }
       }
       float p[U][HG];
@@ -592,11 +619,13 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   }
 
   // ---- combine the lane groups of this workgroup (log-sum-exp).
+  // The running maxima are wavefront-wide: m[r] is the same on every lane
+  // that holds the same head in slot r, and lane 0 holds head r in slot r.
   // Softmax sums per slot: in quad mode a lane holds only its own head's sum
-  // (slot 0) and takes slot r's from the lane r positions ahead.  m and these
-  // sums are equal on the lanes of a group that hold the same head in the same
-  // slot, which the lanes sharing a slice do, so reducing over the lanes of
-  // one slice covers every group once.  Lane 0 holds head r in slot r.
+  // (slot 0) and takes slot r's from the lane r positions ahead.  The sums are
+  // equal on the lanes of a group that hold the same head in the same slot,
+  // which the lanes sharing a slice do, so reducing over the lanes of one
+  // slice covers every group once.
   float ls[HG];
 #pragma unroll
   for (int r = 0; r < HG; ++r) {
@@ -606,10 +635,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       ls[r] = lsum[r];
   }
 #pragma unroll
-  for (int r = 0; r < HG; ++r) {
-    const float mw = strided_reduce<LPT, OpMax>(m[r]);
-    if (lane == 0) s_mw[wave][r] = mw;
-  }
+  for (int r = 0; r < HG; ++r)
+    if (lane == 0) s_mw[wave][r] = m[r];
   __syncthreads();
   float buf[NV];
 #pragma unroll

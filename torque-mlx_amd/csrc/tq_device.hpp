@@ -307,6 +307,19 @@ __device__ __forceinline__ uint32_t unpack_code(const uint32_t* __restrict__ row
 // the slice's raw bits from the row, `decode` turns them into kSliceDims
 // float32 values using an LDS lookup table built from the centroids.
 
+// ---- raw buffer loads.  A buffer resource bounds what a loop may read:
+// a load whose bytes lie past num_records returns zeros and touches no
+// memory, so rows past the end of a range need no clamp.  Untyped loads on
+// this target take DATA_FORMAT = 32 bits in the descriptor's last word.
+constexpr int kBufferWord3 = 0x00020000;
+using BufferRsrc = __amdgpu_buffer_rsrc_t;
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ BufferRsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferWord3);
+}
+
 // 4-bit: 16 dims = 8 bytes = words 2s, 2s+1; one table entry per byte holds
 // the centroids of its low and high nibble.
 struct PackedB4 {
@@ -326,6 +339,11 @@ struct PackedB4 {
   __device__ static float first_centroid(const LutT& t) { return t.x; }
   __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
     const uint2 v = *reinterpret_cast<const uint2*>(row + 8 * slice);
+    return {v.x, v.y};
+  }
+  __device__ static int slice_offset(int slice) { return 8 * slice; }
+  __device__ static Raw load(BufferRsrc r, int off) {
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
     return {v.x, v.y};
   }
   __device__ static void decode(const Raw& r, int /*slice*/, const LutT* __restrict__ lut, float (&x)[kSliceDims]) {
@@ -361,6 +379,8 @@ struct PackedB2 {
   __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
     return {*reinterpret_cast<const uint32_t*>(row + 4 * slice)};
   }
+  __device__ static int slice_offset(int slice) { return 4 * slice; }
+  __device__ static Raw load(BufferRsrc r, int off) { return {__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)}; }
   __device__ static void decode(const Raw& r, int /*slice*/, const LutT* __restrict__ lut, float (&x)[kSliceDims]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -395,6 +415,11 @@ struct PackedB3 {
     const uint32_t* w = reinterpret_cast<const uint32_t*>(row) + ((3 * slice) >> 1);
     return {w[0], w[1]};
   }
+  __device__ static int slice_offset(int slice) { return 4 * ((3 * slice) >> 1); }
+  __device__ static Raw load(BufferRsrc r, int off) {
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return {v.x, v.y};
+  }
   __device__ static void decode(const Raw& r, int slice, const LutT* __restrict__ lut, float (&x)[kSliceDims]) {
     const uint64_t z = ((static_cast<uint64_t>(r.b) << 32) | r.a) >> ((slice & 1) * 16);
 #pragma unroll
@@ -425,6 +450,11 @@ struct DenseF16 {
   __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
     return {*reinterpret_cast<const uint4*>(row + 16 * slice)};
   }
+  __device__ static int slice_offset(int slice) { return 16 * slice; }
+  __device__ static Raw load(BufferRsrc r, int off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return {make_uint4(v.x, v.y, v.z, v.w)};
+  }
   __device__ static void decode(const Raw& r, int, const LutT*, float (&x)[kSliceDims]) {
     const uint32_t w[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
 #pragma unroll
@@ -453,6 +483,11 @@ struct DenseF32 {
   __device__ static float first_centroid(const LutT& t) { return t; }
   __device__ static Raw load(const uint8_t* __restrict__ row, int slice) {
     return {*reinterpret_cast<const float4*>(row + 16 * slice)};
+  }
+  __device__ static int slice_offset(int slice) { return 16 * slice; }
+  __device__ static Raw load(BufferRsrc r, int off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return {make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w))};
   }
   __device__ static void decode(const Raw& r, int, const LutT*, float (&x)[kSliceDims]) {
     x[0] = r.v.x;
