@@ -204,8 +204,8 @@ struct DecodeArgs {
 // A[D]: accumulator relative to max M (log2 units), L: softmax sum.
 template <int D>
 __device__ __forceinline__ void finish_row(const float* A, float M, float L, const float* qs, const float* ck,
-                                           const float* cv, int inverse, const float* signs_left,
-                                           const float* signs_right, float sqrt_d, float* dst) {
+                                           const float* cv, int inverse, const float (&sg_left)[D / kWave],
+                                           const float (&sg_right)[D / kWave], float sqrt_d, float* dst) {
   constexpr int E = D / kWave;
   const int lane = lane_id();
   float e[E];
@@ -225,7 +225,7 @@ __device__ __forceinline__ void finish_row(const float* A, float M, float L, con
   }
 #pragma unroll
   for (int i = 0; i < E; ++i) e[i] = L > 0.f ? e[i] / L : 0.f;
-  if (inverse) wave_rotate<D>(e, signs_left, signs_right, sqrt_d);
+  if (inverse) wave_rotate_signs<D>(e, sg_left, sg_right, sqrt_d);
 #pragma unroll
   for (int i = 0; i < E; ++i) dst[lane * E + i] = e[i];
 }
@@ -381,7 +381,9 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       for (int i = 0; i < E / 2; ++i) qw[i] = q[i];
     }
   }
-  if ((wave < HG && a.rotate_query) || appender) {
+  // Signs are kept in registers: the query rotation uses (right, left), the
+  // inverse rotation of the result (left, right).
+  if ((wave < HG && (a.rotate_query || a.inverse_output)) || appender) {
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       sg_first[i] = a.signs_right[lane * E + i];
@@ -621,41 +623,32 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // ---- combine the lane groups of this workgroup (log-sum-exp).
   // The running maxima are wavefront-wide: m[r] is the same on every lane
   // that holds the same head in slot r, and lane 0 holds head r in slot r.
-  // Softmax sums per slot: in quad mode a lane holds only its own head's sum
-  // (slot 0) and takes slot r's from the lane r positions ahead.  The sums are
-  // equal on the lanes of a group that hold the same head in the same slot,
-  // which the lanes sharing a slice do, so reducing over the lanes of one
-  // slice covers every group once.
-  float ls[HG];
+  // So the lane groups' sums share one reference per head and add without
+  // rescaling: the softmax sums over the lanes of one slice (in quad mode a
+  // lane holds only its own head's sum and takes slot r's from the lane r
+  // positions ahead; the sums are equal on the lanes of a group that hold the
+  // same head in the same slot), the accumulators by a reduce-scatter.  The
+  // wavefronts' partials are weighted against the workgroup maximum when
+  // they are added after the barrier.
 #pragma unroll
   for (int r = 0; r < HG; ++r) {
-    if constexpr (kQuad)
-      ls[r] = r == 0 ? lsum[0] : quad_rotate_to(lsum[0], r);
-    else
-      ls[r] = lsum[r];
-  }
-#pragma unroll
-  for (int r = 0; r < HG; ++r)
-    if (lane == 0) s_mw[wave][r] = m[r];
-  __syncthreads();
-  float buf[NV];
-#pragma unroll
-  for (int r = 0; r < HG; ++r) {
-    const int h = head_of(r);
-    float M = s_mw[0][h];
-#pragma unroll
-    for (int w = 1; w < kWavesPerBlock; ++w) M = fmaxf(M, s_mw[w][h]);
-    const float f = ls[r] > 0.f ? fast_exp2(m[r] - M) : 0.f;
-    const float lw = strided_reduce<LPT, OpSum>(ls[r] * f);
-    if (lane == 0) s_lw[wave][r] = lw;
-#pragma unroll
-    for (int k = 0; k < SD; ++k) buf[r * SD + k] = acc[r][k] * f;
+    const float ls = !kQuad || r == 0 ? lsum[kQuad ? 0 : r] : quad_rotate_to(lsum[0], r);
+    const float lw = strided_reduce<LPT, OpSum>(ls);
+    if (lane == 0) {
+      s_mw[wave][r] = m[r];
+      s_lw[wave][r] = lw;
+    }
   }
   // Reduce-scatter the accumulators over the TPW lane groups of the
   // wavefront: afterwards lane (gi, slice) holds values
   // [gi * NV / TPW, (gi + 1) * NV / TPW) of its slice, summed over groups.
-  if constexpr (TPW > 1) reduce_scatter<LPT, kWave / 2, NV / 2, NV>(buf, lane);
   {
+    float buf[NV];
+#pragma unroll
+    for (int r = 0; r < HG; ++r)
+#pragma unroll
+      for (int k = 0; k < SD; ++k) buf[r * SD + k] = acc[r][k];
+    if constexpr (TPW > 1) reduce_scatter<LPT, kWave / 2, NV / 2, NV>(buf, lane);
     constexpr int W = NV / TPW;
 #pragma unroll
     for (int k = 0; k < W; ++k) {
@@ -665,32 +658,43 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     }
   }
   __syncthreads();
-  float M[HG];  // workgroup maximum of each head
+  // Weight of each wavefront's partial for head h against the workgroup
+  // maximum (zero for a wavefront that saw no token); returns that maximum.
+  auto wave_weights = [&](int h, float (&f)[kWavesPerBlock]) {
+    float M = s_mw[0][h];
 #pragma unroll
-  for (int h = 0; h < HG; ++h) {
-    M[h] = s_mw[0][h];
+    for (int w = 1; w < kWavesPerBlock; ++w) M = fmaxf(M, s_mw[w][h]);
 #pragma unroll
-    for (int w = 1; w < kWavesPerBlock; ++w) M[h] = fmaxf(M[h], s_mw[w][h]);
-  }
+    for (int w = 0; w < kWavesPerBlock; ++w) f[w] = s_mw[w][h] == -INFINITY ? 0.f : fast_exp2(s_mw[w][h] - M);
+    return M;
+  };
+  // Sum of the wavefronts' accumulators into s_red[0], weighted.
+  auto combine_waves = [&]() {
+    for (int o = tid; o < HG * D; o += kBlock) {
+      float f[kWavesPerBlock];
+      wave_weights(o / D, f);
+      float v = s_red[0][o] * f[0];
+#pragma unroll
+      for (int w = 1; w < kWavesPerBlock; ++w) v = fmaf(s_red[w][o], f[w], v);
+      s_red[0][o] = v;
+    }
+    __syncthreads();
+  };
 
   // ---- one split: this workgroup holds the whole result and finishes it.
   const int64_t qhg0 = static_cast<int64_t>(layer) * a.query_heads + qh0;
   if (a.n_splits == 1) {
-    for (int o = tid; o < HG * D; o += kBlock) {
-      float v = s_red[0][o];
-#pragma unroll
-      for (int w = 1; w < kWavesPerBlock; ++w) v += s_red[w][o];
-      s_red[0][o] = v;
-    }
-    __syncthreads();
+    combine_waves();
     if (wave < HG) {
-      float l = s_lw[0][wave];
+      float f[kWavesPerBlock];
+      const float M = wave_weights(wave, f);
+      float l = 0.f;
 #pragma unroll
-      for (int w = 1; w < kWavesPerBlock; ++w) l += s_lw[w][wave];
+      for (int w = 0; w < kWavesPerBlock; ++w) l = fmaf(s_lw[w][wave], f[w], l);
       const float* ck = appending ? s_cur[0] : a.cur_k ? a.cur_k + static_cast<int64_t>(lkv) * D : nullptr;
       const float* cv = appending ? s_cur[1] : a.cur_v ? a.cur_v + static_cast<int64_t>(lkv) * D : nullptr;
-      finish_row<D>(&s_red[0][wave * D], M[wave], l, s_q[wave], ck, cv, a.inverse_output, a.signs_left,
-                    a.signs_right, a.sqrt_d, a.out + (qhg0 + wave) * D);
+      finish_row<D>(&s_red[0][wave * D], M, l, s_q[wave], ck, cv, a.inverse_output, sg_second, sg_first, a.sqrt_d,
+                    a.out + (qhg0 + wave) * D);
     }
     return;
   }
@@ -699,26 +703,22 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // accumulator is stored inverse-rotated already: the rotation is linear, so
   // the merge is a plain weighted sum per dimension.  Split 0 also publishes
   // the current token's score per query head and its value per KV head.
-  for (int o = tid; o < HG * D; o += kBlock) {
-    float v = s_red[0][o];
-#pragma unroll
-    for (int w = 1; w < kWavesPerBlock; ++w) v += s_red[w][o];
-    s_red[0][o] = v;
-  }
-  __syncthreads();
+  combine_waves();
   if (wave < HG) {
     float e[E];
 #pragma unroll
     for (int i = 0; i < E; ++i) e[i] = s_red[0][wave * D + lane * E + i];
-    if (a.inverse_output) wave_rotate<D>(e, a.signs_left, a.signs_right, a.sqrt_d);
+    if (a.inverse_output) wave_rotate_signs<D>(e, sg_second, sg_first, a.sqrt_d);
     float* dst = a.ws_acc + ((qhg0 + wave) * a.n_splits + split) * D + lane * E;
 #pragma unroll
     for (int i = 0; i < E; ++i) dst[i] = e[i];
     if (lane == 0) {
-      float l = s_lw[0][wave];
+      float f[kWavesPerBlock];
+      const float M = wave_weights(wave, f);
+      float l = 0.f;
 #pragma unroll
-      for (int w = 1; w < kWavesPerBlock; ++w) l += s_lw[w][wave];
-      a.ws_ml[((qhg0 + wave) * a.n_splits + split) * 2] = M[wave];
+      for (int w = 0; w < kWavesPerBlock; ++w) l = fmaf(s_lw[w][wave], f[w], l);
+      a.ws_ml[((qhg0 + wave) * a.n_splits + split) * 2] = M;
       a.ws_ml[((qhg0 + wave) * a.n_splits + split) * 2 + 1] = l;
     }
     if (split == 0 && (appending || a.cur_k != nullptr)) {
@@ -733,7 +733,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
         const float* cv = (appending ? s_cur[1] : a.cur_v + static_cast<int64_t>(lkv) * D) + lane * E;
 #pragma unroll
         for (int i = 0; i < E; ++i) v[i] = cv[i];
-        if (a.inverse_output) wave_rotate<D>(v, a.signs_left, a.signs_right, a.sqrt_d);
+        if (a.inverse_output) wave_rotate_signs<D>(v, sg_second, sg_first, a.sqrt_d);
 #pragma unroll
         for (int i = 0; i < E; ++i) a.ws_cur_v[static_cast<int64_t>(lkv) * D + lane * E + i] = v[i];
       }
