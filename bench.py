@@ -220,7 +220,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
     stores = [c._store for c in caches]
     w = stores[0].layout.packed_words
     n_splits = [ops.plan_splits(1, hkv, hq, d, s0 + steps, dev) for _ in range(L)]
-    ws = ops.workspace_for(1, hkv, hq, d, 0, dev)
+    ws = ops.workspace_for(1, hkv, hq, d, args.splits, dev)
     out = torch.empty((L, hq, d), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     lib = _lib.load()
@@ -237,7 +237,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
                 queries[t, l].data_ptr(), new_k[t, l].data_ptr(), new_v[t, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d,
                 bits, st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, seq,
                 st.key_centroids.data_ptr(), st.value_centroids.data_ptr(), st.key_boundaries.data_ptr(),
-                st.value_boundaries.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), rot, dflags, 0,
+                st.value_boundaries.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), rot, dflags, args.splits,
                 ws.data_ptr(), out[l].data_ptr(), stream)))
             unfused_step.append((lib.tq_append, (
                 new_k[t, l].data_ptr(), new_v[t, l].data_ptr(), _lib.TQ_F16, 1, hkv, 1, d, bits, st.signs_left.data_ptr(),
@@ -247,7 +247,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
                 queries[t, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d, bits, st.key_codes.data_ptr(),
                 st.value_codes.data_ptr(), st.capacity, seq + 1, st.key_centroids.data_ptr(),
                 st.value_centroids.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), dflags, None, None,
-                0, ws.data_ptr(), out[l].data_ptr(), stream)))
+                args.splits, ws.data_ptr(), out[l].data_ptr(), stream)))
         calls.append(fused_step)
         calls_unfused.append(unfused_step)
 
@@ -355,7 +355,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
             "bits": bits,
             "prefill": s0,
             "query_dtype": "f16",
-            "n_splits_at_prefill": n_splits[0],
+            "n_splits_at_prefill": args.splits or n_splits[0],
             "step": "per layer: tq_decode_append (pack the new token and decode with it) + merge kernel",
         },
         "step_us_mean": round(mean_us, 2),
