@@ -71,6 +71,7 @@ constexpr float kRescaleThreshold = 8.0f;
 constexpr int kMaxSplits = 256;
 constexpr int kTokensPerIter = 2;  // tokens per lane group per loop iteration
 constexpr int kPrefetchIters = 1;  // loop iterations whose loads are in flight ahead
+constexpr int kScoreChains = 4;    // independent score product chains per token (matrix-core mode)
 
 // ============================================================== rotation
 
@@ -245,7 +246,7 @@ __device__ __forceinline__ float scatter_pair(float x, float y, int lane) {
     const bool upper = (lane & LM) != 0;
     const float send = upper ? x : y;
     const float keep = upper ? y : x;
-    return keep + __shfl_xor(send, LM);
+    return keep + xor_partner<LM>(send, lane);
   }
 }
 
@@ -259,6 +260,25 @@ __device__ __forceinline__ void reduce_scatter(float (&buf)[NV], int lane) {
 #pragma unroll
   for (int k = 0; k < LEN; ++k) buf[k] = scatter_pair<LM>(buf[k], buf[k + LEN], lane);
   if constexpr (LM > LO) reduce_scatter<LO, LM / 2, LEN / 2, NV>(buf, lane);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Matrix-core score products leave on lane l, register i, the partial score
+// of token 4 * ((l / 4) / LPT) + i over slice (l / 4) % LPT.  Sum over the
+// LPT slices (lane bits 2 .. 2 + log2(LPT) - 1) and keep on lane l the token
+// of its value layout, l / LPT, i.e. register (l / LPT) % 4: a reduce-scatter
+// over lane bits log2(LPT) + 1 and log2(LPT) (which select that register)
+// and an all-reduce over the slice bits below them.
+template <int LPT>
+__device__ __forceinline__ float slice_sum_select(f32x4 c, int lane) {
+  static_assert(LPT == 4 || LPT == 8 || LPT == 16, "4, 8 or 16 slices per token");
+  float buf[4] = {c[0], c[1], c[2], c[3]};
+  reduce_scatter<LPT, 2 * LPT, 2, 4>(buf, lane);
+  float v = buf[0];
+  if constexpr (LPT >= 8) v += xor_partner<4>(v, lane);
+  if constexpr (LPT >= 16) v += xor_partner<8>(v, lane);
+  return v;
 }
 
 template <class Fmt, int D, int HG, bool QF16>
@@ -318,19 +338,48 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // in the resource base (scalar arithmetic), the lane's part in a fixed
   // per-token offset, and rows past the end of the split read as zeros and
   // are masked out when processed, so loads need no clamp and no branch.
-  int lane_off[U];
+  //
+  // Matrix-core mode (packed rows, groups of 4 query heads): scores and value
+  // updates run as 4x4x1 fp32 outer products (v_mfma_f32_4x4x1_16b_f32, 16
+  // blocks of 4 lanes; block b = lanes 4b..4b+3, output element (i, j) of a
+  // block in register i of lane 4b + j, A operand of row i from lane 4b + i,
+  // B operand of column j from lane 4b + j).  Key rows are then read in a
+  // second lane layout: a lane quad holds 4 consecutive tokens of one slice
+  // (lane l: token 4 * ((l / 4) / LPT) + l % 4, slice (l / 4) % LPT), so one
+  // product per slice dimension gives 4 tokens x 4 heads of partial scores.
+  // Value rows keep the token-major layout (lane l: token l / LPT, slice
+  // l % LPT), where a quad holds 4 slices of one token and one product per
+  // slice dimension adds weight(head i) x value(dim of lane j).
+  constexpr bool kMfma = Fmt::kHasLut && HG == 4;
+  const int tk = kMfma ? 4 * ((lane >> 2) / LPT) + (lane & 3) : gi;
+  const int sk = kMfma ? (lane >> 2) % LPT : slice;
+  int lane_off_k[U], lane_off_v[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) lane_off[u] = (wave * TPW + u * TPB + gi) * ROW + Fmt::slice_offset(slice);
+  for (int u = 0; u < U; ++u) {
+    lane_off_k[u] = (wave * TPW + u * TPB + tk) * ROW + Fmt::slice_offset(sk);
+    lane_off_v[u] = (wave * TPW + u * TPB + gi) * ROW + Fmt::slice_offset(slice);
+  }
+  // Every iteration's loads are issued unconditionally -- an iteration past
+  // the end of the split gets an empty range and reads zeros without touching
+  // memory -- so the compiler can count the loads in flight and wait only for
+  // the iteration being processed, not for the prefetched ones.
+  auto iter_rsrc = [&](const uint8_t* base, int i) {
+    const int64_t row0 = min(t0 + static_cast<int64_t>(i) * STRIDE, static_cast<int64_t>(t1));
+    return make_rsrc(base + row0 * ROW, static_cast<uint32_t>(t1 - row0) * ROW);
+  };
+  auto load_k = [&](int i, Raw (&kr)[U]) {
+    const BufferRsrc rk = iter_rsrc(kbase, i);
+#pragma unroll
+    for (int u = 0; u < U; ++u) kr[u] = Fmt::load(rk, lane_off_k[u]);
+  };
+  auto load_v = [&](int i, Raw (&vr)[U]) {
+    const BufferRsrc rv = iter_rsrc(vbase, i);
+#pragma unroll
+    for (int u = 0; u < U; ++u) vr[u] = Fmt::load(rv, lane_off_v[u]);
+  };
   auto load_iter = [&](int i, Raw (&kr)[U], Raw (&vr)[U]) {
-    const int64_t row0 = t0 + static_cast<int64_t>(i) * STRIDE;
-    const uint32_t bytes = static_cast<uint32_t>(t1 - row0) * ROW;
-    const BufferRsrc rk = make_rsrc(kbase + row0 * ROW, bytes);
-    const BufferRsrc rv = make_rsrc(vbase + row0 * ROW, bytes);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      kr[u] = Fmt::load(rk, lane_off[u]);
-      vr[u] = Fmt::load(rv, lane_off[u]);
-    }
+    load_k(i, kr);
+    load_v(i, vr);
   };
 
   // ---- set-up loads first: this thread's centroid-table entry, the query
@@ -396,8 +445,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // PF iterations are requested here, so their latency overlaps the set-up.
   Raw kr[NB][U], vr[NB][U];
 #pragma unroll
-  for (int j = 0; j < PF; ++j)
-    if (j < n_iter) load_iter(j, kr[j], vr[j]);
+  for (int j = 0; j < PF; ++j) load_iter(j, kr[j], vr[j]);
 
   // ---- centroid tables
   if constexpr (Fmt::kHasLut) {
@@ -452,28 +500,116 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // in the odd quads of a token's lanes makes the row_half_mirror / row_mirror
   // partners (quad position p <-> 3 - p) own the same head.  Other modes use
   // slot r = head r.
-  constexpr bool kQuad = HG == 4;
+  constexpr bool kQuad = HG == 4 && !kMfma;
   const int q4 = lane & 3;
   const int slot_x = (kQuad && LPT >= 8 && ((lane >> 2) & 1)) ? 3 : 0;
   auto head_of = [&](int r) { return kQuad ? (((q4 + r) & 3) ^ slot_x) : r; };
 
   float qv[HG][SD];
+  if constexpr (!kMfma) {
 #pragma unroll
-  for (int r = 0; r < HG; ++r)
+    for (int r = 0; r < HG; ++r)
 #pragma unroll
-    for (int i = 0; i < SD; ++i) qv[r][i] = s_q[head_of(r)][slice * SD + i];
+      for (int i = 0; i < SD; ++i) qv[r][i] = s_q[head_of(r)][slice * SD + i];
+  }
 
   float m[HG], lsum[HG], acc[HG][SD];
 #pragma unroll
   for (int r = 0; r < HG; ++r) {
     m[r] = -INFINITY;
-    lsum[r] = 0.f;  // quad mode uses lsum[0] for the lane's own head
+    lsum[r] = 0.f;  // quad and matrix-core modes use lsum[0] for the lane's own head
 #pragma unroll
     for (int i = 0; i < SD; ++i) acc[r][i] = 0.f;
   }
 
+  // Matrix-core mode: the lane's query slice of head lane % 4 (the B operand
+  // of the score products), and the value accumulators cv[k] = (head 0..3) at
+  // dimension slice * SD + k.  m[0] and lsum[0] belong to head lane % 4 and
+  // the lane's value token; m[0] is wavefront-wide per head.
+  float qk[SD];
+  f32x4 cv[SD];
+  if constexpr (kMfma) {
+#pragma unroll
+    for (int k = 0; k < SD; ++k) {
+      qk[k] = s_q[lane & 3][sk * SD + k];
+      cv[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
   const typename Fmt::LutT* lut_k = s_lut[0];
   const typename Fmt::LutT* lut_v = s_lut[1];
+
+  // Matrix-core mode, three parts of an iteration.  score_products: the
+  // 4 x 4 x 1 products of one iteration's key rows, kScoreChains independent
+  // chains per token (dimension k goes to chain k % kScoreChains).
+  // score_reduce: the chains and then the slices are summed and each lane
+  // keeps the score of its own (head, value token).  softmax_values: online
+  // softmax update and value products of one iteration.
+  constexpr int SC = kScoreChains;
+  auto score_products = [&](const Raw (&kr)[U], f32x4 (&c)[U][SC]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float x[SD];
+      Fmt::decode(kr[u], sk, lut_k, x);
+#pragma unroll
+      for (int k = 0; k < SD; ++k)
+        c[u][k % SC] = __builtin_amdgcn_mfma_f32_4x4x1f32(x[k], qk[k], k < SC ? f32x4{0.f, 0.f, 0.f, 0.f} : c[u][k % SC],
+                                                          0, 0, 0);
+    }
+  };
+  auto score_reduce = [&](f32x4 (&c)[U][SC], float (&s_own)[U]) {
+    if constexpr (kMfma) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int w = SC / 2; w >= 1; w /= 2)
+#pragma unroll
+          for (int j = 0; j < w; ++j) c[u][j] += c[u][j + w];
+        s_own[u] = slice_sum_select<LPT>(c[u][0], lane);
+      }
+    }
+  };
+  auto softmax_values = [&](const Raw (&vr)[U], const float (&s_own)[U], int i, auto full) {
+    constexpr bool FULL = decltype(full)::value;
+    bool valid[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) valid[u] = FULL || first + i * STRIDE + u * TPB + gi < t1;
+    float xv[U][SD];
+#pragma unroll
+    for (int u = 0; u < U; ++u) Fmt::decode(vr[u], slice, lut_v, xv[u]);
+    bool need = false;
+#pragma unroll
+    for (int u = 0; u < U; ++u) need = need || (valid[u] && s_own[u] > m[0] + kRescaleThreshold);
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      // A running maximum moves: one maximum per head over the wavefront
+      // (lanes sharing lane % 4), accumulators of head r rescaled by the
+      // factor of the lanes that hold head r.
+      float mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u) mx = valid[u] ? fmaxf(mx, s_own[u]) : mx;
+      mx = strided_reduce<4, OpMax>(mx);
+      float alpha = 1.f;
+      if (mx > m[0] + kRescaleThreshold) {
+        alpha = fast_exp2(m[0] - mx);  // 0 before the first maximum: nothing accumulated yet
+        m[0] = mx;
+      }
+      lsum[0] *= alpha;
+      const float a0 = quad_broadcast_t<0>(alpha), a1 = quad_broadcast_t<1>(alpha);
+      const float a2 = quad_broadcast_t<2>(alpha), a3 = quad_broadcast_t<3>(alpha);
+#pragma unroll
+      for (int k = 0; k < SD; ++k) cv[k] *= f32x4{a0, a1, a2, a3};
+    }
+    float p[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      p[u] = valid[u] ? fast_exp2(s_own[u] - m[0]) : 0.f;
+      lsum[0] += p[u];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int k = 0; k < SD; ++k) cv[k] = __builtin_amdgcn_mfma_f32_4x4x1f32(p[u], xv[u][k], cv[k], 0, 0, 0);
+  };
 
   // Partial dot products of this lane's slice: part[u][s] for token u, slot s.
   auto partial_scores = [&](const Raw (&kr)[U], float (&part)[U][HG]) {
@@ -607,16 +743,30 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     }
   };
 
+  // The ring is unrolled NB times with no exit inside it (an iteration past
+  // n_iter reads nothing and masks every token), so the waits for each slot
+  // are the same on every trip and leave the PF prefetched slots in flight.
   for (int it = 0; it < n_iter; it += NB) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int i = it + j;
-      if (i >= n_iter) break;
-      if (i + PF < n_iter) load_iter(i + PF, kr[(j + PF) % NB], vr[(j + PF) % NB]);
-      if (first + i * STRIDE + (U - 1) * TPB + TPW <= t1)
-        process(kr[j], vr[j], i, std::true_type{});
-      else
-        process(kr[j], vr[j], i, std::false_type{});
+      load_iter(i + PF, kr[(j + PF) % NB], vr[(j + PF) % NB]);
+      const bool full = first + i * STRIDE + (U - 1) * TPB + TPW <= t1;
+      if constexpr (kMfma) {
+        f32x4 c[U][SC];
+        float s_own[U];
+        score_products(kr[j], c);
+        score_reduce(c, s_own);
+        if (full)
+          softmax_values(vr[j], s_own, i, std::true_type{});
+        else
+          softmax_values(vr[j], s_own, i, std::false_type{});
+      } else {
+        if (full)
+          process(kr[j], vr[j], i, std::true_type{});
+        else
+          process(kr[j], vr[j], i, std::false_type{});
+      }
     }
   }
 
@@ -630,13 +780,24 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // same head in the same slot), the accumulators by a reduce-scatter.  The
   // wavefronts' partials are weighted against the workgroup maximum when
   // they are added after the barrier.
+  if constexpr (kMfma) {
+    // Matrix-core mode: lane l holds head l % 4 and value token l / LPT; the
+    // LPT / 4 lanes of a token that hold the same head add each weight once.
+    const float ls = (lane % LPT) < 4 ? lsum[0] : 0.f;
+    const float lw = strided_reduce<4, OpSum>(ls);
+    if (lane < 4) {
+      s_mw[wave][lane] = m[0];
+      s_lw[wave][lane] = lw;
+    }
+  } else {
 #pragma unroll
-  for (int r = 0; r < HG; ++r) {
-    const float ls = !kQuad || r == 0 ? lsum[kQuad ? 0 : r] : quad_rotate_to(lsum[0], r);
-    const float lw = strided_reduce<LPT, OpSum>(ls);
-    if (lane == 0) {
-      s_mw[wave][r] = m[r];
-      s_lw[wave][r] = lw;
+    for (int r = 0; r < HG; ++r) {
+      const float ls = !kQuad || r == 0 ? lsum[kQuad ? 0 : r] : quad_rotate_to(lsum[0], r);
+      const float lw = strided_reduce<LPT, OpSum>(ls);
+      if (lane == 0) {
+        s_mw[wave][r] = m[r];
+        s_lw[wave][r] = lw;
+      }
     }
   }
   // Reduce-scatter the accumulators over the TPW lane groups of the
@@ -647,7 +808,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int r = 0; r < HG; ++r)
 #pragma unroll
-      for (int k = 0; k < SD; ++k) buf[r * SD + k] = acc[r][k];
+      for (int k = 0; k < SD; ++k) buf[r * SD + k] = kMfma ? cv[k][r] : acc[r][k];
     if constexpr (TPW > 1) reduce_scatter<LPT, kWave / 2, NV / 2, NV>(buf, lane);
     constexpr int W = NV / TPW;
 #pragma unroll
