@@ -71,7 +71,7 @@ constexpr float kRescaleThreshold = 8.0f;
 constexpr int kMaxSplits = 256;
 constexpr int kTokensPerIter = 2;  // tokens per lane group per loop iteration
 constexpr int kPrefetchIters = 1;  // loop iterations whose loads are in flight ahead
-constexpr int kScoreChains = 4;    // independent score product chains per token (matrix-core mode)
+constexpr int kScoreChains = 2;    // independent score product chains per token (matrix-core mode)
 constexpr bool kPhaseFences = true;  // matrix-core mode: no interleaving of products with VALU work
 
 // ============================================================== rotation
