@@ -87,7 +87,10 @@ int tq_quantize_dequantize(const void* keys, const void* values, int dtype, int6
 int tq_unpack_dequantize(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, int head_dim,
                          int bits, const float* centroids, float* out, hipStream_t stream);
 
-/* Split count the decode kernels use when n_splits <= 0 is passed. */
+/* Split count the decode kernels use when n_splits <= 0 is passed.  The
+ * sequence is dealt out to the splits in blocks of one workgroup iteration
+ * (split s takes blocks s, s + n, s + 2n, ...); an explicit n_splits above
+ * the number of blocks is lowered to it. */
 int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int head_dim, int64_t seq_len,
                              int num_cus);
 

@@ -9,11 +9,13 @@
 //                        place into the [L, Hkv, capacity, W] slab
 //   unpack_kernel        packed slab -> dense float32 centroid values
 //   decode_kernel<Fmt>   split-K decode attention: each workgroup owns one
-//                        (layer, KV head, query-head group) and one contiguous
-//                        sequence split and writes its partial (max, sum,
-//                        accumulator); with a single split it finishes the
-//                        rows itself.  Fmt selects packed 2/3/4-bit or dense
-//                        fp16/fp32 rows.
+//                        (layer, KV head, query-head group) and one split of
+//                        the sequence (row blocks dealt out cyclically) and
+//                        writes its partial (max, sum, accumulator); with a
+//                        single split it finishes the rows itself.  Fmt
+//                        selects packed 2/3/4-bit or dense fp16/fp32 rows;
+//                        packed rows with groups of 4 query heads run their
+//                        products on the matrix cores.
 //   merge_kernel         log-sum-exp merge of the splits of one query head,
 //                        current token, normalisation, inverse rotation.
 //   score / softmax / accumulate kernels   the three stages of the
