@@ -35,6 +35,7 @@ sys.path.insert(0, str(REPO))
 
 METRIC = "packed decode-attn µs/step + achieved HBM GB/s (% peak) at 4-bit, 32K ctx"
 HBM_PEAK_GBPS = 8000.0
+FP32_MATRIX_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 
 WORKLOADS = {
     # name: (layers, kv_heads, query_heads, head_dim, bits, seq_len, std, description)
@@ -562,6 +563,18 @@ def main() -> int:
             "traffic_source": traffic_src,
             "kernel": kernel_name,
             "algorithmic_bytes_per_launch": algo_bytes,
+        },
+        # The same kernel against its arithmetic ceiling: 4 L Hq S D flops per
+        # step (a multiply-add per query head and packed code for the score
+        # and for the value update), fp32, which the split kernel runs as
+        # 4x4x1 fp32 products on the matrix cores for groups of 4 query heads.
+        "roofline_compute": {
+            "bound": "mfma",
+            "achieved": round(4 * L * hq * s * d / (kern_us * 1e-6) / 1e12, 2),
+            "peak": FP32_MATRIX_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(4 * L * hq * s * d / (kern_us * 1e-6) / 1e12 / FP32_MATRIX_PEAK_TFLOPS, 4),
+            "flops_per_launch": 4 * L * hq * s * d,
         },
     }
 
