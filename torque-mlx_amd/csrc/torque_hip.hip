@@ -883,18 +883,24 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // accumulator is stored inverse-rotated already: the rotation is linear, so
   // the merge is a plain weighted sum per dimension.  Split 0 also publishes
   // the current token's score per query head and its value per KV head.
-  combine_waves();
+  // Wavefront h < HG sums head h's row over the 4 wavefronts' partials
+  // straight from LDS (no combining pass, no second barrier).
   if (wave < HG) {
+    float f[kWavesPerBlock];
+    const float M = wave_weights(wave, f);
     float e[E];
 #pragma unroll
-    for (int i = 0; i < E; ++i) e[i] = s_red[0][wave * D + lane * E + i];
+    for (int i = 0; i < E; ++i) {
+      float v = s_red[0][wave * D + lane * E + i] * f[0];
+#pragma unroll
+      for (int w = 1; w < kWavesPerBlock; ++w) v = fmaf(s_red[w][wave * D + lane * E + i], f[w], v);
+      e[i] = v;
+    }
     if (a.inverse_output) wave_rotate_signs<D>(e, sg_second, sg_first, a.sqrt_d);
     float* dst = a.ws_acc + ((qhg0 + wave) * a.n_splits + split) * D + lane * E;
 #pragma unroll
     for (int i = 0; i < E; ++i) dst[i] = e[i];
     if (lane == 0) {
-      float f[kWavesPerBlock];
-      const float M = wave_weights(wave, f);
       float l = 0.f;
 #pragma unroll
       for (int w = 0; w < kWavesPerBlock; ++w) l = fmaf(s_lw[w][wave], f[w], l);
