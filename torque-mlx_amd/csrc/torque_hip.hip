@@ -1394,19 +1394,30 @@ int with_d(int head_dim, Args&&... args) {
   return fail(TQ_ERR_UNSUPPORTED, "Unsupported head dimension: " + std::to_string(head_dim));
 }
 
+// Workgroups per launch of the row kernels (fwht, append, unpack).  A HIP
+// launch holds at most 2^32 - 1 work-items; larger calls are cut into
+// launches of at most this many workgroups, in stream order.
+constexpr int64_t kMaxLaunchBlocks = int64_t(1) << 20;
+
 template <int D>
 struct FwhtBody {
   static int run(const void* x, int x_dtype, float* y, int64_t rows, const float* s_first, const float* s_second,
                  hipStream_t stream) {
-    const int64_t nblk = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
     const float sd = sqrt_f32(D);
-    if (x_dtype == TQ_F16)
-      hipLaunchKernelGGL((fwht_kernel<D, __half>), dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0, stream,
-                         static_cast<const __half*>(x), y, rows, s_first, s_second, sd);
-    else
-      hipLaunchKernelGGL((fwht_kernel<D, float>), dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0, stream,
-                         static_cast<const float*>(x), y, rows, s_first, s_second, sd);
-    return launch_status("fwht_kernel");
+    const int64_t chunk = kMaxLaunchBlocks * kWavesPerBlock;  // one wavefront per row
+    for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+      const int64_t n = std::min(chunk, rows - r0);
+      const unsigned nblk = static_cast<unsigned>((n + kWavesPerBlock - 1) / kWavesPerBlock);
+      if (x_dtype == TQ_F16)
+        hipLaunchKernelGGL((fwht_kernel<D, __half>), dim3(nblk), dim3(kBlock), 0, stream,
+                           static_cast<const __half*>(x) + r0 * D, y + r0 * D, n, s_first, s_second, sd);
+      else
+        hipLaunchKernelGGL((fwht_kernel<D, float>), dim3(nblk), dim3(kBlock), 0, stream,
+                           static_cast<const float*>(x) + r0 * D, y + r0 * D, n, s_first, s_second, sd);
+      const int rc = launch_status("fwht_kernel");
+      if (rc) return rc;
+    }
+    return TQ_OK;
   }
 };
 
@@ -1432,30 +1443,55 @@ struct AppendParams {
   bool dequant;
 };
 
+// One launch over rows [g0 * seq_new + t0, + rows) of p: `groups` whole
+// (layer, head) groups from group g0 (t0 = 0), or `rows` tokens of group g0
+// from token t0.
 template <int D, int BITS, typename T, bool DQ>
-void launch_append(const AppendParams& p, hipStream_t stream) {
-  const int64_t items = p.rows * p.streams;
-  const int64_t nblk = (items + kWavesPerBlock - 1) / kWavesPerBlock;
+int launch_append_part(const AppendParams& p, int64_t g0, int64_t t0, int64_t seq_part, int64_t rows,
+                       hipStream_t stream) {
+  constexpr int W = D * BITS / 32;
+  const int64_t row0 = g0 * p.seq_new + t0;
+  const int64_t nblk = (rows * p.streams + kWavesPerBlock - 1) / kWavesPerBlock;
   hipLaunchKernelGGL((append_kernel<D, BITS, T, DQ>), dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0, stream,
-                     static_cast<const T*>(p.keys), static_cast<const T*>(p.values), p.rows, p.streams, p.seq_new,
-                     p.rotate_keys, p.rotate_values, p.signs_left, p.signs_right, sqrt_f32(D), p.key_bnd,
-                     p.value_bnd, p.key_cent, p.value_cent, p.key_codes, p.value_codes, p.capacity, p.offset,
-                     p.key_out, p.value_out);
+                     static_cast<const T*>(p.keys) + row0 * D, static_cast<const T*>(p.values) + row0 * D, rows,
+                     p.streams, seq_part, p.rotate_keys, p.rotate_values, p.signs_left, p.signs_right, sqrt_f32(D),
+                     p.key_bnd, p.value_bnd, p.key_cent, p.value_cent,
+                     p.key_codes ? p.key_codes + g0 * p.capacity * W : nullptr,
+                     p.value_codes ? p.value_codes + g0 * p.capacity * W : nullptr, p.capacity, p.offset + t0,
+                     p.key_out ? p.key_out + row0 * D : nullptr, p.value_out ? p.value_out + row0 * D : nullptr);
+  return launch_status("append_kernel");
+}
+
+// rows = groups * seq_new items per stream; at most kMaxLaunchBlocks
+// workgroups per launch, cut at whole groups, or at tokens when one group
+// alone is larger.
+template <int D, int BITS, typename T, bool DQ>
+int launch_append(const AppendParams& p, hipStream_t stream) {
+  const int64_t max_rows = kMaxLaunchBlocks * kWavesPerBlock / p.streams;
+  const int64_t groups = p.rows / p.seq_new;
+  if (p.seq_new <= max_rows) {
+    const int64_t per = max_rows / p.seq_new;
+    for (int64_t g0 = 0; g0 < groups; g0 += per) {
+      const int64_t ng = std::min(per, groups - g0);
+      const int rc = launch_append_part<D, BITS, T, DQ>(p, g0, 0, p.seq_new, ng * p.seq_new, stream);
+      if (rc) return rc;
+    }
+    return TQ_OK;
+  }
+  for (int64_t g = 0; g < groups; ++g)
+    for (int64_t t0 = 0; t0 < p.seq_new; t0 += max_rows) {
+      const int64_t nt = std::min(max_rows, p.seq_new - t0);
+      const int rc = launch_append_part<D, BITS, T, DQ>(p, g, t0, nt, nt, stream);
+      if (rc) return rc;
+    }
+  return TQ_OK;
 }
 
 template <int D, int BITS>
-void append_dtype(const AppendParams& p, hipStream_t stream) {
-  if (p.dtype == TQ_F16) {
-    if (p.dequant)
-      launch_append<D, BITS, __half, true>(p, stream);
-    else
-      launch_append<D, BITS, __half, false>(p, stream);
-  } else {
-    if (p.dequant)
-      launch_append<D, BITS, float, true>(p, stream);
-    else
-      launch_append<D, BITS, float, false>(p, stream);
-  }
+int append_dtype(const AppendParams& p, hipStream_t stream) {
+  if (p.dtype == TQ_F16)
+    return p.dequant ? launch_append<D, BITS, __half, true>(p, stream) : launch_append<D, BITS, __half, false>(p, stream);
+  return p.dequant ? launch_append<D, BITS, float, true>(p, stream) : launch_append<D, BITS, float, false>(p, stream);
 }
 
 template <int D>
@@ -1463,18 +1499,14 @@ struct AppendBody {
   static int run(const AppendParams& p, int bits, hipStream_t stream) {
     switch (bits) {
       case 2:
-        append_dtype<D, 2>(p, stream);
-        break;
+        return append_dtype<D, 2>(p, stream);
       case 3:
-        append_dtype<D, 3>(p, stream);
-        break;
+        return append_dtype<D, 3>(p, stream);
       case 4:
-        append_dtype<D, 4>(p, stream);
-        break;
+        return append_dtype<D, 4>(p, stream);
       default:
         return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
     }
-    return launch_status("append_kernel");
   }
 };
 
@@ -1516,28 +1548,53 @@ struct StageBody {
 
 template <int D>
 struct UnpackBody {
+  // One launch: `groups` groups of seq_len tokens (group stride `capacity`
+  // rows) into out [groups, seq_len, D].
+  template <int BITS>
+  static int part(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, const float* cent,
+                  float* out, hipStream_t stream) {
+    const unsigned nblk = static_cast<unsigned>((groups * seq_len * D + kBlock - 1) / kBlock);
+    hipLaunchKernelGGL(unpack_kernel<BITS>, dim3(nblk), dim3(kBlock), 0, stream, codes, groups, capacity, seq_len, D,
+                       cent, out);
+    return launch_status("unpack_kernel");
+  }
+  // At most kMaxLaunchBlocks workgroups (one thread per output value) per
+  // launch: cut at whole groups, or at tokens when one group alone is larger.
+  template <int BITS>
+  static int chunks(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, const float* cent,
+                    float* out, hipStream_t stream) {
+    constexpr int W = D * BITS / 32;
+    const int64_t max_tokens = kMaxLaunchBlocks * kBlock / D;
+    if (seq_len <= max_tokens) {
+      const int64_t per = max_tokens / seq_len;
+      for (int64_t g0 = 0; g0 < groups; g0 += per) {
+        const int64_t ng = std::min(per, groups - g0);
+        const int rc = part<BITS>(codes + g0 * capacity * W, ng, capacity, seq_len, cent, out + g0 * seq_len * D, stream);
+        if (rc) return rc;
+      }
+      return TQ_OK;
+    }
+    for (int64_t g = 0; g < groups; ++g)
+      for (int64_t t0 = 0; t0 < seq_len; t0 += max_tokens) {
+        const int64_t nt = std::min(max_tokens, seq_len - t0);
+        const int rc = part<BITS>(codes + (g * capacity + t0) * W, 1, capacity, nt, cent,
+                                  out + (g * seq_len + t0) * D, stream);
+        if (rc) return rc;
+      }
+    return TQ_OK;
+  }
   static int run(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, int bits,
                  const float* cent, float* out, hipStream_t stream) {
-    const int64_t total = groups * seq_len * D;
-    const int64_t nblk = (total + kBlock - 1) / kBlock;
-    if (nblk == 0) return TQ_OK;
     switch (bits) {
       case 2:
-        hipLaunchKernelGGL(unpack_kernel<2>, dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0, stream, codes, groups,
-                           capacity, seq_len, D, cent, out);
-        break;
+        return chunks<2>(codes, groups, capacity, seq_len, cent, out, stream);
       case 3:
-        hipLaunchKernelGGL(unpack_kernel<3>, dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0, stream, codes, groups,
-                           capacity, seq_len, D, cent, out);
-        break;
+        return chunks<3>(codes, groups, capacity, seq_len, cent, out, stream);
       case 4:
-        hipLaunchKernelGGL(unpack_kernel<4>, dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0, stream, codes, groups,
-                           capacity, seq_len, D, cent, out);
-        break;
+        return chunks<4>(codes, groups, capacity, seq_len, cent, out, stream);
       default:
         return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
     }
-    return launch_status("unpack_kernel");
   }
 };
 
