@@ -74,6 +74,24 @@ def test_decode_argument_errors(args, code, message):
     assert message in lib.tq_last_error().decode()
 
 
+@pytest.mark.parametrize(
+    ("num_layers", "seq_len", "n_splits", "message"),
+    [
+        (1 << 22, 10, 0, "exceeds one launch"),  # 2^25 (layer, head group) units > 2^24 workgroups
+        (1 << 19, 100_000, 8, "exceeds one merge launch"),  # 2^19 x 32 heads x 4 merge groups > 2^24
+    ],
+)
+def test_decode_launch_size_errors(num_layers, seq_len, n_splits, message):
+    from torque_hip import _lib
+
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    rc = lib.tq_decode(fake, 0, num_layers, 32, 8, 128, 4, fake, fake, seq_len, seq_len, fake, fake, None, None, 0,
+                       None, None, n_splits, fake, fake, None)
+    assert rc == -1
+    assert message in lib.tq_last_error().decode()
+
+
 def test_status_mapping():
     from torque_hip import _lib
 

@@ -1181,11 +1181,16 @@ int make_plan(int num_layers, int kv_heads, int query_heads, int64_t seq_len, in
   const int group = query_heads / kv_heads;
   p->hg = pick_hg(group);
   p->n_hgroups = group / p->hg;
-  p->units = num_layers * kv_heads * p->n_hgroups;
+  // One launch holds at most 2^32 - 1 work-items: units x splits workgroups.
+  const int64_t max_wg = ((int64_t(1) << 32) - 1) / kBlock;
+  const int64_t units = static_cast<int64_t>(num_layers) * kv_heads * p->n_hgroups;
+  if (units > max_wg)
+    return fail(TQ_ERR_BAD_ARG, "num_layers x kv_heads x head groups exceeds one launch; decode fewer layers per call");
+  p->units = static_cast<int>(units);
   int ns = n_splits > 0 ? n_splits : default_splits(p->units, seq_len, device_cu_count());
   if (ns > kMaxSplits) return fail(TQ_ERR_BAD_ARG, "n_splits must be at most " + std::to_string(kMaxSplits));
   const int64_t blocks = std::max<int64_t>(1, (seq_len + block_rows - 1) / block_rows);
-  p->n_splits = static_cast<int>(std::min<int64_t>(blocks, ns));
+  p->n_splits = static_cast<int>(std::min<int64_t>({blocks, static_cast<int64_t>(ns), max_wg / units}));
   return TQ_OK;
 }
 
@@ -1288,6 +1293,9 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   const int block_rows = kTokensPerIter * kWavesPerBlock * kWave * slice_dims / head_dim;
   rc = make_plan(num_layers, kv_heads, query_heads, seq_len, n_splits, block_rows, &p);
   if (rc) return rc;
+  if (p.n_splits > 1 &&
+      static_cast<int64_t>(num_layers) * query_heads * (head_dim / kMergeDims) > ((int64_t(1) << 32) - 1) / kBlock)
+    return fail(TQ_ERR_BAD_ARG, "num_layers x query_heads exceeds one merge launch; decode fewer layers per call");
 
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const WsLayout wl = workspace_layout(static_cast<int64_t>(num_layers) * query_heads,
