@@ -16,8 +16,9 @@
 //                        selects packed 2/3/4-bit or dense fp16/fp32 rows;
 //                        packed rows with groups of 4 query heads run their
 //                        products on the matrix cores.
-//   merge_kernel         log-sum-exp merge of the splits of one query head,
-//                        current token, normalisation, inverse rotation.
+//   merge_kernel         log-sum-exp merge of the splits of one query head
+//                        (partials arrive rotated back), current token,
+//                        normalisation.
 //   score / softmax / accumulate kernels   the three stages of the
 //                        reference's split path, for profiling and the op API.
 
