@@ -72,6 +72,19 @@ int tq_append(const void* keys, const void* values, int dtype, int num_layers, i
               const float* key_boundaries, const float* value_boundaries, uint32_t* key_codes,
               uint32_t* value_codes, int64_t capacity, int64_t offset, hipStream_t stream);
 
+/* Per-vector scales (opt-in extension; the reference has none -- its codes
+ * index one global codebook per stream, quantization.py:120-148).  The
+ * rotated row x is quantized as x / s with s = sqrt(mean(x^2)) (1 for a zero
+ * row), one float32 s per (layer, KV head, token) and stream, stored in scale
+ * slabs [L, Hkv, capacity] beside the code slabs.  The codes equal the
+ * reference packer applied to x / s; the dequantized token is centroid x s.
+ * Same arguments as tq_append plus the two scale slabs. */
+int tq_append_scaled(const void* keys, const void* values, int dtype, int num_layers, int kv_heads, int64_t seq_new,
+                     int head_dim, int bits, const float* signs_left, const float* signs_right, int flags,
+                     const float* key_boundaries, const float* value_boundaries, uint32_t* key_codes,
+                     uint32_t* value_codes, float* key_scales, float* value_scales, int64_t capacity,
+                     int64_t offset, hipStream_t stream);
+
 /* Rotate (per flags) -> quantize -> dequantize to dense float32 centroid values,
  * rows [rows, D] -> out [rows, D]; values/value_out may be NULL.  Replaces
  * TorqueKVCacheMLX._quantize_rows on the current token (cache_mlx.py:246-255, 496-502). */
@@ -81,11 +94,25 @@ int tq_quantize_dequantize(const void* keys, const void* values, int dtype, int6
                            const float* key_centroids, const float* value_centroids, float* key_out,
                            float* value_out, hipStream_t stream);
 
+/* tq_quantize_dequantize with per-vector scales (see tq_append_scaled):
+ * out = centroid(code(x / s)) x s.  The current token of a scaled cache. */
+int tq_quantize_dequantize_scaled(const void* keys, const void* values, int dtype, int64_t rows, int head_dim,
+                                  int bits, const float* signs_left, const float* signs_right, int flags,
+                                  const float* key_boundaries, const float* value_boundaries,
+                                  const float* key_centroids, const float* value_centroids, float* key_out,
+                                  float* value_out, hipStream_t stream);
+
 /* Unpack + dequantize the first seq_len tokens of `groups` slab rows:
  * codes [groups, capacity, W] -> out float32 [groups, seq_len, D].
  * Replaces TorqueKVCache.export_dequantized (cache.py:189-214). */
 int tq_unpack_dequantize(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, int head_dim,
                          int bits, const float* centroids, float* out, hipStream_t stream);
+
+/* tq_unpack_dequantize of a scaled slab: out = centroid x scale, scales
+ * [groups, capacity] float32 (see tq_append_scaled). */
+int tq_unpack_dequantize_scaled(const uint32_t* codes, const float* scales, int64_t groups, int64_t capacity,
+                                int64_t seq_len, int head_dim, int bits, const float* centroids, float* out,
+                                hipStream_t stream);
 
 /* Split count the decode kernels use when n_splits <= 0 is passed.  The
  * sequence is dealt out to the splits in blocks of one workgroup iteration
@@ -117,6 +144,18 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
               int64_t seq_len, const float* key_centroids, const float* value_centroids,
               const float* signs_left, const float* signs_right, int flags, const float* current_keys,
               const float* current_values, int n_splits, void* workspace, float* out, hipStream_t stream);
+
+/* tq_decode over slabs written by tq_append_scaled: a token's score is
+ * multiplied by its key scale and its value by its value scale (scales
+ * [L, Hkv, capacity] float32).  current_keys / current_values, when given,
+ * are already scaled (tq_quantize_dequantize_scaled).  No counterpart in the
+ * reference, which has no per-vector scales. */
+int tq_decode_scaled(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads, int head_dim,
+                     int bits, const uint32_t* key_codes, const uint32_t* value_codes, const float* key_scales,
+                     const float* value_scales, int64_t capacity, int64_t seq_len, const float* key_centroids,
+                     const float* value_centroids, const float* signs_left, const float* signs_right, int flags,
+                     const float* current_keys, const float* current_values, int n_splits, void* workspace,
+                     float* out, hipStream_t stream);
 
 /* Append one token to the packed slabs and decode with it in one launch:
  * the same as tq_append(new token at row seq_len) followed by

@@ -27,6 +27,13 @@ Every function cites the reference file:line it restates (paths relative to
   round trip, straddle positions.
 * ``streaming_attention_decode``  -- textbook softmax attention in float64,
   single-token closed form, empty-sequence zeros.
+* ``rms_scales`` / ``quantize_scaled`` / ``dequantize_scaled`` -- the opt-in
+  per-vector scale extension, which has NO reference counterpart (the
+  reference's codes index one global codebook, quantization.py:120-148):
+  pinned by closed forms (constant rows, zero rows), exact invariance of the
+  codes under power-of-two scaling of a row, and the Lloyd-Max distortion of
+  N(0, 1) that the normalisation is for (reconstruction error of rows with
+  widely varying norms).
 """
 
 from __future__ import annotations
@@ -178,6 +185,32 @@ def quantize_boundary_count(values: np.ndarray, boundaries: np.ndarray) -> np.nd
 def dequantize(indices: np.ndarray, centroids: np.ndarray) -> np.ndarray:
     """quantization.py:151-153."""
     return np.asarray(centroids, dtype=np.float32)[np.asarray(indices)].astype(np.float32)
+
+
+# ---------------------------------------------------------------- per-vector scales (extension)
+
+
+def rms_scales(values: np.ndarray) -> np.ndarray:
+    """Per-row scale of ``scale_mode="rms"`` (no reference counterpart): float32 sqrt(mean(x^2)) over the
+    last axis, 1 for an all-zero row."""
+    v = np.asarray(values, dtype=np.float32).astype(np.float64)
+    rms = np.sqrt(np.mean(v * v, axis=-1)).astype(np.float32)
+    return np.where(rms > 0, rms, np.float32(1.0)).astype(np.float32)
+
+
+def quantize_scaled(
+    values: np.ndarray, boundaries: np.ndarray, scales: np.ndarray | None = None
+) -> tuple[np.ndarray, np.ndarray]:
+    """Codes of each row divided by its scale (float32 division; the reference's boundary count,
+    quantization.py:139-148, applied to x / s) and the scales; ``scales`` defaults to ``rms_scales``."""
+    v = np.asarray(values, dtype=np.float32)
+    s = rms_scales(v) if scales is None else np.asarray(scales, dtype=np.float32)
+    return quantize_boundary_count((v / s[..., None]).astype(np.float32), boundaries), s
+
+
+def dequantize_scaled(indices: np.ndarray, centroids: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """Centroid x per-row scale, float32."""
+    return (dequantize(indices, centroids) * np.asarray(scales, dtype=np.float32)[..., None]).astype(np.float32)
 
 
 # ---------------------------------------------------------------- bit packing

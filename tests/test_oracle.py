@@ -177,6 +177,54 @@ def test_error_budget():
     assert float(np.mean((rotated - recon) ** 2)) < 0.05
 
 
+# ------------------------------------------------------------------ per-vector scales (extension)
+
+
+def test_rms_scales_closed_forms():
+    rows = np.full((3, 64), -2.5, dtype=np.float32)
+    rows[1] = 0.0
+    rows[2] = np.tile(np.array([3.0, -4.0], dtype=np.float32), 32)  # mean square 12.5
+    s = o.rms_scales(rows)
+    assert s[0] == np.float32(2.5)
+    assert s[1] == np.float32(1.0)  # an all-zero row keeps scale 1 (codes of 0)
+    assert s[2] == np.float32(np.sqrt(12.5))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_scaled_codes_invariant_under_power_of_two_scaling(bits):
+    # x * 2^k has scale s * 2^k exactly, and (x * 2^k) / (s * 2^k) == x / s exactly in float32.
+    rng = np.random.default_rng(4)
+    cb = o.build_gaussian_codebook(bits)
+    bnd = o.codebook_boundaries(cb)
+    x = (rng.normal(size=(300, 128)) * rng.lognormal(0.0, 2.0, size=(300, 1))).astype(np.float32)
+    codes, s = o.quantize_scaled(x, bnd)
+    for k in (-7, 3, 12):
+        c2, s2 = o.quantize_scaled(x * np.float32(2.0**k), bnd)
+        np.testing.assert_array_equal(c2, codes)
+        np.testing.assert_array_equal(s2, s * np.float32(2.0**k))
+    # Without the division the codes are not scale invariant.
+    assert not np.array_equal(o.quantize_boundary_count(x * np.float32(8.0), bnd), o.quantize_boundary_count(x, bnd))
+
+
+@pytest.mark.parametrize(("bits", "lloyd_max_mse"), [(2, 0.1175), (3, 0.03455), (4, 0.009497)])
+def test_scaled_quantization_error_matches_lloyd_max(bits, lloyd_max_mse):
+    # Max (1960): the least mean-square error of a 2^b-level quantizer of N(0, 1).  Rows N(0, sigma^2) with
+    # sigma spanning four decades quantize to that error relative to their power once divided by their RMS;
+    # with one global codebook and no scale they do not.
+    rng = np.random.default_rng(5)
+    cb = o.build_gaussian_codebook(bits)
+    bnd = o.codebook_boundaries(cb)
+    sigma = np.exp(rng.uniform(np.log(1e-2), np.log(1e2), size=(2000, 1)))
+    x = (rng.normal(size=(2000, 128)) * sigma).astype(np.float32)
+    codes, s = o.quantize_scaled(x, bnd)
+    rec = o.dequantize_scaled(codes, cb, s)
+    rel = np.mean((rec - x) ** 2, axis=1) / np.mean(x**2, axis=1)
+    assert abs(float(rel.mean()) / lloyd_max_mse - 1.0) < 0.1
+    plain = o.dequantize(o.quantize_boundary_count(x, bnd), cb)
+    rel_plain = np.mean((plain - x) ** 2, axis=1) / np.mean(x**2, axis=1)
+    assert float(rel_plain.mean()) > 10 * float(rel.mean())
+
+
 # ------------------------------------------------------------------ rotation
 
 

@@ -103,14 +103,18 @@ __global__ __launch_bounds__(kBlock) void fwht_kernel(const T* __restrict__ x, f
 
 // One wavefront per (row, stream).  Items [0, rows) are keys, [rows, 2 rows)
 // values (when `streams` == 2).  Rows are (l, h, t) in [L, Hkv, seq_new] order.
-template <int D, int BITS, typename T, bool DEQUANT>
+// SCALED (per-vector scales): the rotated row x is quantized as x / s with
+// s = sqrt(mean(x^2)) (1 for a zero row); s is stored at the token's slot of
+// the [L, Hkv, capacity] scale slab, or multiplied into the dequantized
+// values.
+template <int D, int BITS, typename T, bool DEQUANT, bool SCALED>
 __global__ __launch_bounds__(kBlock) void append_kernel(
     const T* __restrict__ keys, const T* __restrict__ values, int64_t rows, int streams, int64_t seq_new,
     int rotate_keys, int rotate_values, const float* __restrict__ signs_left, const float* __restrict__ signs_right,
     float sqrt_d, const float* __restrict__ key_bnd, const float* __restrict__ value_bnd,
     const float* __restrict__ key_cent, const float* __restrict__ value_cent, uint32_t* __restrict__ key_codes,
     uint32_t* __restrict__ value_codes, int64_t capacity, int64_t offset, float* __restrict__ key_out,
-    float* __restrict__ value_out) {
+    float* __restrict__ value_out, float* __restrict__ key_scales, float* __restrict__ value_scales) {
   constexpr int E = D / kWave;
   constexpr int W = D * BITS / 32;
   __shared__ uint8_t s_codes[kWavesPerBlock][D];
@@ -119,6 +123,7 @@ __global__ __launch_bounds__(kBlock) void append_kernel(
   const bool active = item < rows * streams;
   const bool is_v = item >= rows;
   const int64_t r = is_v ? item - rows : item;
+  float scale = 1.f;  // per-vector scale (SCALED)
   if (active) {
     const T* src = (is_v ? values : keys) + r * D + lane * E;
     float v[E];
@@ -126,11 +131,22 @@ __global__ __launch_bounds__(kBlock) void append_kernel(
     for (int i = 0; i < E; ++i) v[i] = to_f32(src[i]);
     if (is_v ? rotate_values : rotate_keys) wave_rotate<D>(v, signs_right, signs_left, sqrt_d);
     const float* bnd = is_v ? value_bnd : key_bnd;
+    if constexpr (SCALED) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) ss = fmaf(v[i], v[i], ss);
+      ss = group_sum<kWave>(ss);
+      const float rms = sqrtf(ss / static_cast<float>(D));
+      scale = rms > 0.f ? rms : 1.f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) v[i] = v[i] / scale;
+    }
     if constexpr (DEQUANT) {
       const float* cent = is_v ? value_cent : key_cent;
       float* dst = (is_v ? value_out : key_out) + r * D + lane * E;
 #pragma unroll
-      for (int i = 0; i < E; ++i) dst[i] = cent[quantize_count<BITS>(v[i], bnd)];
+      for (int i = 0; i < E; ++i) dst[i] = SCALED ? cent[quantize_count<BITS>(v[i], bnd)] * scale
+                                                  : cent[quantize_count<BITS>(v[i], bnd)];
     } else {
 #pragma unroll
       for (int i = 0; i < E; ++i) s_codes[wave][lane * E + i] = static_cast<uint8_t>(quantize_count<BITS>(v[i], bnd));
@@ -143,6 +159,7 @@ __global__ __launch_bounds__(kBlock) void append_kernel(
       const int64_t lh = r / seq_new, t = r - lh * seq_new;
       uint32_t* dst = (is_v ? value_codes : key_codes) + (lh * capacity + offset + t) * W + lane;
       *dst = word;
+      if (SCALED && lane == 0) (is_v ? value_scales : key_scales)[lh * capacity + offset + t] = scale;
     }
   }
 }
@@ -150,10 +167,12 @@ __global__ __launch_bounds__(kBlock) void append_kernel(
 // ============================================================== unpack
 
 
+// scales (or null): per-token scale slab [groups, capacity] multiplied in.
 template <int BITS>
 __global__ __launch_bounds__(kBlock) void unpack_kernel(const uint32_t* __restrict__ codes, int64_t groups,
                                                         int64_t capacity, int64_t seq_len, int head_dim,
-                                                        const float* __restrict__ cent, float* __restrict__ out) {
+                                                        const float* __restrict__ cent,
+                                                        const float* __restrict__ scales, float* __restrict__ out) {
   const int W = head_dim * BITS / 32;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   const int64_t total = groups * seq_len * head_dim;
@@ -162,7 +181,8 @@ __global__ __launch_bounds__(kBlock) void unpack_kernel(const uint32_t* __restri
   const int64_t tok = idx / head_dim;
   const int64_t g = tok / seq_len, t = tok - g * seq_len;
   const uint32_t* row = codes + (g * capacity + t) * W;
-  out[idx] = cent[unpack_code<BITS>(row, d)];
+  const float c = cent[unpack_code<BITS>(row, d)];
+  out[idx] = scales != nullptr ? c * scales[g * capacity + t] : c;
 }
 
 // ============================================================== decode
@@ -201,6 +221,11 @@ struct DecodeArgs {
   float* ws_cur_s; // [L * Hq]              score of the current token (log2 units)
   float* ws_cur_v; // [L * Hkv, D]          current token's value, rotated back when requested
   float* out;     // [L, Hq, D]
+  // Per-vector scales (SCALED kernels): [L, Hkv, cap] float32 per stream; a
+  // token's score is multiplied by its key scale, its value by its value
+  // scale.
+  const float* k_scales;
+  const float* v_scales;
 };
 
 // Finish one output row held by a wavefront: optional extra dense token
@@ -284,7 +309,7 @@ __device__ __forceinline__ float slice_sum_select(f32x4 c, int lane) {
   return v;
 }
 
-template <class Fmt, int D, int HG, bool QF16>
+template <class Fmt, int D, int HG, bool QF16, bool SCALED>
 __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   constexpr int SD = Fmt::kSliceDims;
   constexpr int LPT = D / SD;        // lanes per token
@@ -388,9 +413,25 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) vr[u] = Fmt::load(rv, lane_off_v[u]);
   };
-  auto load_iter = [&](int i, Raw (&kr)[U], Raw (&vr)[U]) {
+  // Scaled mode: the key and value scales of the lane's value tokens
+  // (lane group gi), loaded with the rows they belong to.
+  const float* ksbase = SCALED ? a.k_scales + static_cast<int64_t>(lkv) * a.cap : nullptr;
+  const float* vsbase = SCALED ? a.v_scales + static_cast<int64_t>(lkv) * a.cap : nullptr;
+  auto load_scales = [&](int i, float (&ks)[U], float (&vs)[U]) {
+    const int64_t row0 = min(t0 + static_cast<int64_t>(i) * BSTRIDE, static_cast<int64_t>(t1));
+    const uint32_t bytes = static_cast<uint32_t>(t1 - row0) * 4u;
+    const BufferRsrc rk = make_rsrc(ksbase + row0, bytes), rv = make_rsrc(vsbase + row0, bytes);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int off = (wave * TPW + u * TPB + gi) * 4;
+      ks[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rk, off, 0, 0));
+      vs[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
+    }
+  };
+  auto load_iter = [&](int i, Raw (&kr)[U], Raw (&vr)[U], float (&ks)[U], float (&vs)[U]) {
     load_k(i, kr);
     load_v(i, vr);
+    if constexpr (SCALED) load_scales(i, ks, vs);
   };
 
   // ---- set-up loads first: this thread's centroid-table entry, the query
@@ -455,8 +496,9 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // iteration i + PF are in flight while iteration i is processed.  The first
   // PF iterations are requested here, so their latency overlaps the set-up.
   Raw kr[NB][U], vr[NB][U];
+  float ksr[NB][U], vsr[NB][U];  // scaled mode only
 #pragma unroll
-  for (int j = 0; j < PF; ++j) load_iter(j, kr[j], vr[j]);
+  for (int j = 0; j < PF; ++j) load_iter(j, kr[j], vr[j], ksr[j], vsr[j]);
 
   // ---- centroid tables
   if constexpr (Fmt::kHasLut) {
@@ -587,7 +629,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       }
     }
   };
-  auto softmax_values = [&](const Raw (&vr)[U], const float (&s_own)[U], int i, auto full) {
+  auto softmax_values = [&](const Raw (&vr)[U], const float (&s_own)[U], const float (&vs)[U], int i, auto full) {
     constexpr bool FULL = decltype(full)::value;
     bool valid[U];
 #pragma unroll
@@ -622,6 +664,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     for (int u = 0; u < U; ++u) {
       p[u] = valid[u] ? fast_exp2(s_own[u] - m[0]) : 0.f;
       lsum[0] += p[u];
+      if constexpr (SCALED) p[u] *= vs[u];  // the value products take weight x value scale
     }
     if constexpr (kPhaseFences) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -650,7 +693,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // One iteration: U tokens per lane group -- U x HG partial scores, their
   // reduction over the group's lanes, one online-softmax update per head and
   // U value updates.  FULL iterations skip the validity masks.
-  auto process = [&](const Raw (&kr)[U], const Raw (&vr)[U], int i, auto full) {
+  auto process = [&](const Raw (&kr)[U], const Raw (&vr)[U], const float (&ks)[U], const float (&vs)[U], int i,
+                     auto full) {
     constexpr bool FULL = decltype(full)::value;
     bool valid[U];
 #pragma unroll
@@ -673,6 +717,10 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       for (int u = 0; u < U; ++u)
         own[u] = cross_quad_sum<LPT>(part[u][0] + quad_rotate_from<1>(part[u][1]) + quad_rotate_from<2>(part[u][2]) +
                                      quad_rotate_from<3>(part[u][3]));
+      if constexpr (SCALED) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) own[u] *= ks[u];
+      }
       bool need = false;
 #pragma unroll
       for (int u = 0; u < U; ++u) need = need || (valid[u] && own[u] > m[0] + kRescaleThreshold);
@@ -706,6 +754,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
       for (int u = 0; u < U; ++u) {
         p_own[u] = valid[u] ? fast_exp2(own[u] - m[0]) : 0.f;
         lsum[0] += p_own[u];
+        if constexpr (SCALED) p_own[u] *= vs[u];
       }
 #pragma unroll
       for (int u = 0; u < U; ++u)
@@ -720,7 +769,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int s = 0; s < HG; ++s) part[u][s] = group_sum<LPT>(part[u][s]);
+        for (int s = 0; s < HG; ++s) part[u][s] = SCALED ? group_sum<LPT>(part[u][s]) * ks[u] : group_sum<LPT>(part[u][s]);
       // Wavefront-wide running maxima, moved only when some score passes
       // one by more than the threshold (as in quad mode).
       bool need = false;
@@ -753,6 +802,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
         for (int s = 0; s < HG; ++s) {
           p[u][s] = valid[u] ? fast_exp2(part[u][s] - m[s]) : 0.f;
           lsum[s] += p[u][s];
+          if constexpr (SCALED) p[u][s] *= vs[u];
         }
 #pragma unroll
       for (int u = 0; u < U; ++u)
@@ -770,22 +820,26 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int i = it + j;
-      load_iter(i + PF, kr[(j + PF) % NB], vr[(j + PF) % NB]);
+      load_iter(i + PF, kr[(j + PF) % NB], vr[(j + PF) % NB], ksr[(j + PF) % NB], vsr[(j + PF) % NB]);
       const bool full = first + i * BSTRIDE + (U - 1) * TPB + TPW <= t1;
       if constexpr (kMfma) {
         f32x4 c[U][SC];
         float s_own[U];
         score_products(kr[j], c);
         score_reduce(c, s_own);
+        if constexpr (SCALED) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) s_own[u] *= ksr[j][u];
+        }
         if (full)
-          softmax_values(vr[j], s_own, i, std::true_type{});
+          softmax_values(vr[j], s_own, vsr[j], i, std::true_type{});
         else
-          softmax_values(vr[j], s_own, i, std::false_type{});
+          softmax_values(vr[j], s_own, vsr[j], i, std::false_type{});
       } else {
         if (full)
-          process(kr[j], vr[j], i, std::true_type{});
+          process(kr[j], vr[j], ksr[j], vsr[j], i, std::true_type{});
         else
-          process(kr[j], vr[j], i, std::false_type{});
+          process(kr[j], vr[j], ksr[j], vsr[j], i, std::false_type{});
       }
     }
   }
@@ -1195,20 +1249,31 @@ int make_plan(int num_layers, int kv_heads, int query_heads, int64_t seq_len, in
   return TQ_OK;
 }
 
-template <class Fmt, int D, int HG, bool QF16>
+template <class Fmt, int D, int HG, bool QF16, bool SC>
 void launch_decode_q(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (start != nullptr || stop != nullptr)
-    hipExtLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16>), dim3(nblk), dim3(kBlock), 0, stream, start, stop, 0, a);
+    hipExtLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16, SC>), dim3(nblk), dim3(kBlock), 0, stream, start, stop, 0,
+                          a);
   else
-    hipLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16>), dim3(nblk), dim3(kBlock), 0, stream, a);
+    hipLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16, SC>), dim3(nblk), dim3(kBlock), 0, stream, a);
+}
+
+// Scaled kernels exist for packed rows only (the host never passes scales
+// with dense rows).
+template <class Fmt, int D, int HG, bool QF16>
+void launch_decode_s(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  if constexpr (Fmt::kHasLut) {
+    if (a.k_scales != nullptr) return launch_decode_q<Fmt, D, HG, QF16, true>(a, nblk, stream, start, stop);
+  }
+  launch_decode_q<Fmt, D, HG, QF16, false>(a, nblk, stream, start, stop);
 }
 
 template <class Fmt, int D, int HG>
 void launch_decode(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (a.q_f16)
-    launch_decode_q<Fmt, D, HG, true>(a, nblk, stream, start, stop);
+    launch_decode_s<Fmt, D, HG, true>(a, nblk, stream, start, stop);
   else
-    launch_decode_q<Fmt, D, HG, false>(a, nblk, stream, start, stop);
+    launch_decode_s<Fmt, D, HG, false>(a, nblk, stream, start, stop);
 }
 
 template <class Fmt, int D>
@@ -1258,9 +1323,14 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
                   int head_dim, const void* keys, const void* values, int64_t capacity, int64_t seq_len,
                   const float* cent_k, const float* cent_v, const float* signs_left, const float* signs_right,
                   int flags, const float* cur_k, const float* cur_v, int n_splits, void* workspace, float* out,
-                  hipStream_t stream, hipEvent_t start, hipEvent_t stop, const AppendSpec* app = nullptr) {
+                  hipStream_t stream, hipEvent_t start, hipEvent_t stop, const AppendSpec* app = nullptr,
+                  const float* k_scales = nullptr, const float* v_scales = nullptr) {
   int rc = check_geometry(head_dim, 0);
   if (rc) return rc;
+  if ((k_scales == nullptr) != (v_scales == nullptr))
+    return fail(TQ_ERR_BAD_ARG, "key_scales and value_scales must both be given or both be null");
+  if (k_scales != nullptr && app != nullptr)
+    return fail(TQ_ERR_BAD_ARG, "per-vector scales are not supported by the fused append + decode");
   if (query == nullptr || out == nullptr || workspace == nullptr)
     return fail(TQ_ERR_BAD_ARG, "query, out and workspace must be non-null");
   if (query_dtype != TQ_F32 && query_dtype != TQ_F16) return fail(TQ_ERR_BAD_ARG, "query dtype must be F32 or F16");
@@ -1324,6 +1394,8 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   a.inverse_output = (flags & TQ_INVERSE_OUTPUT) != 0;
   a.cur_k = cur_k;
   a.cur_v = cur_v;
+  a.k_scales = k_scales;
+  a.v_scales = v_scales;
   if (app != nullptr) {
     a.new_k = app->keys;
     a.new_v = app->values;
@@ -1450,31 +1522,38 @@ struct AppendParams {
   float* key_out;
   float* value_out;
   bool dequant;
+  // per-vector scales (scaled mode): scale slabs [L, Hkv, capacity] written
+  // by the packing path; the dequantizing path multiplies them in.
+  bool scaled;
+  float* key_scales;
+  float* value_scales;
 };
 
 // One launch over rows [g0 * seq_new + t0, + rows) of p: `groups` whole
 // (layer, head) groups from group g0 (t0 = 0), or `rows` tokens of group g0
 // from token t0.
-template <int D, int BITS, typename T, bool DQ>
+template <int D, int BITS, typename T, bool DQ, bool SC>
 int launch_append_part(const AppendParams& p, int64_t g0, int64_t t0, int64_t seq_part, int64_t rows,
                        hipStream_t stream) {
   constexpr int W = D * BITS / 32;
   const int64_t row0 = g0 * p.seq_new + t0;
   const int64_t nblk = (rows * p.streams + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL((append_kernel<D, BITS, T, DQ>), dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0, stream,
+  hipLaunchKernelGGL((append_kernel<D, BITS, T, DQ, SC>), dim3(static_cast<unsigned>(nblk)), dim3(kBlock), 0, stream,
                      static_cast<const T*>(p.keys) + row0 * D, static_cast<const T*>(p.values) + row0 * D, rows,
                      p.streams, seq_part, p.rotate_keys, p.rotate_values, p.signs_left, p.signs_right, sqrt_f32(D),
                      p.key_bnd, p.value_bnd, p.key_cent, p.value_cent,
                      p.key_codes ? p.key_codes + g0 * p.capacity * W : nullptr,
                      p.value_codes ? p.value_codes + g0 * p.capacity * W : nullptr, p.capacity, p.offset + t0,
-                     p.key_out ? p.key_out + row0 * D : nullptr, p.value_out ? p.value_out + row0 * D : nullptr);
+                     p.key_out ? p.key_out + row0 * D : nullptr, p.value_out ? p.value_out + row0 * D : nullptr,
+                     p.key_scales ? p.key_scales + g0 * p.capacity : nullptr,
+                     p.value_scales ? p.value_scales + g0 * p.capacity : nullptr);
   return launch_status("append_kernel");
 }
 
 // rows = groups * seq_new items per stream; at most kMaxLaunchBlocks
 // workgroups per launch, cut at whole groups, or at tokens when one group
 // alone is larger.
-template <int D, int BITS, typename T, bool DQ>
+template <int D, int BITS, typename T, bool DQ, bool SC>
 int launch_append(const AppendParams& p, hipStream_t stream) {
   const int64_t max_rows = kMaxLaunchBlocks * kWavesPerBlock / p.streams;
   const int64_t groups = p.rows / p.seq_new;
@@ -1482,7 +1561,7 @@ int launch_append(const AppendParams& p, hipStream_t stream) {
     const int64_t per = max_rows / p.seq_new;
     for (int64_t g0 = 0; g0 < groups; g0 += per) {
       const int64_t ng = std::min(per, groups - g0);
-      const int rc = launch_append_part<D, BITS, T, DQ>(p, g0, 0, p.seq_new, ng * p.seq_new, stream);
+      const int rc = launch_append_part<D, BITS, T, DQ, SC>(p, g0, 0, p.seq_new, ng * p.seq_new, stream);
       if (rc) return rc;
     }
     return TQ_OK;
@@ -1490,17 +1569,22 @@ int launch_append(const AppendParams& p, hipStream_t stream) {
   for (int64_t g = 0; g < groups; ++g)
     for (int64_t t0 = 0; t0 < p.seq_new; t0 += max_rows) {
       const int64_t nt = std::min(max_rows, p.seq_new - t0);
-      const int rc = launch_append_part<D, BITS, T, DQ>(p, g, t0, nt, nt, stream);
+      const int rc = launch_append_part<D, BITS, T, DQ, SC>(p, g, t0, nt, nt, stream);
       if (rc) return rc;
     }
   return TQ_OK;
 }
 
+template <int D, int BITS, typename T>
+int append_mode(const AppendParams& p, hipStream_t stream) {
+  if (p.scaled)
+    return p.dequant ? launch_append<D, BITS, T, true, true>(p, stream) : launch_append<D, BITS, T, false, true>(p, stream);
+  return p.dequant ? launch_append<D, BITS, T, true, false>(p, stream) : launch_append<D, BITS, T, false, false>(p, stream);
+}
+
 template <int D, int BITS>
 int append_dtype(const AppendParams& p, hipStream_t stream) {
-  if (p.dtype == TQ_F16)
-    return p.dequant ? launch_append<D, BITS, __half, true>(p, stream) : launch_append<D, BITS, __half, false>(p, stream);
-  return p.dequant ? launch_append<D, BITS, float, true>(p, stream) : launch_append<D, BITS, float, false>(p, stream);
+  return p.dtype == TQ_F16 ? append_mode<D, BITS, __half>(p, stream) : append_mode<D, BITS, float>(p, stream);
 }
 
 template <int D>
@@ -1561,24 +1645,25 @@ struct UnpackBody {
   // rows) into out [groups, seq_len, D].
   template <int BITS>
   static int part(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, const float* cent,
-                  float* out, hipStream_t stream) {
+                  const float* scales, float* out, hipStream_t stream) {
     const unsigned nblk = static_cast<unsigned>((groups * seq_len * D + kBlock - 1) / kBlock);
     hipLaunchKernelGGL(unpack_kernel<BITS>, dim3(nblk), dim3(kBlock), 0, stream, codes, groups, capacity, seq_len, D,
-                       cent, out);
+                       cent, scales, out);
     return launch_status("unpack_kernel");
   }
   // At most kMaxLaunchBlocks workgroups (one thread per output value) per
   // launch: cut at whole groups, or at tokens when one group alone is larger.
   template <int BITS>
   static int chunks(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, const float* cent,
-                    float* out, hipStream_t stream) {
+                    const float* scales, float* out, hipStream_t stream) {
     constexpr int W = D * BITS / 32;
     const int64_t max_tokens = kMaxLaunchBlocks * kBlock / D;
     if (seq_len <= max_tokens) {
       const int64_t per = max_tokens / seq_len;
       for (int64_t g0 = 0; g0 < groups; g0 += per) {
         const int64_t ng = std::min(per, groups - g0);
-        const int rc = part<BITS>(codes + g0 * capacity * W, ng, capacity, seq_len, cent, out + g0 * seq_len * D, stream);
+        const int rc = part<BITS>(codes + g0 * capacity * W, ng, capacity, seq_len, cent,
+                                  scales ? scales + g0 * capacity : nullptr, out + g0 * seq_len * D, stream);
         if (rc) return rc;
       }
       return TQ_OK;
@@ -1587,25 +1672,111 @@ struct UnpackBody {
       for (int64_t t0 = 0; t0 < seq_len; t0 += max_tokens) {
         const int64_t nt = std::min(max_tokens, seq_len - t0);
         const int rc = part<BITS>(codes + (g * capacity + t0) * W, 1, capacity, nt, cent,
-                                  out + (g * seq_len + t0) * D, stream);
+                                  scales ? scales + g * capacity + t0 : nullptr, out + (g * seq_len + t0) * D, stream);
         if (rc) return rc;
       }
     return TQ_OK;
   }
   static int run(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, int bits,
-                 const float* cent, float* out, hipStream_t stream) {
+                 const float* cent, const float* scales, float* out, hipStream_t stream) {
     switch (bits) {
       case 2:
-        return chunks<2>(codes, groups, capacity, seq_len, cent, out, stream);
+        return chunks<2>(codes, groups, capacity, seq_len, cent, scales, out, stream);
       case 3:
-        return chunks<3>(codes, groups, capacity, seq_len, cent, out, stream);
+        return chunks<3>(codes, groups, capacity, seq_len, cent, scales, out, stream);
       case 4:
-        return chunks<4>(codes, groups, capacity, seq_len, cent, out, stream);
+        return chunks<4>(codes, groups, capacity, seq_len, cent, scales, out, stream);
       default:
         return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
     }
   }
 };
+
+int append_impl(const void* keys, const void* values, int dtype, int num_layers, int kv_heads, int64_t seq_new,
+                int head_dim, int bits, const float* signs_left, const float* signs_right, int flags,
+                const float* key_boundaries, const float* value_boundaries, uint32_t* key_codes,
+                uint32_t* value_codes, int64_t capacity, int64_t offset, float* key_scales, float* value_scales,
+                hipStream_t stream) {
+  int rc = check_geometry(head_dim, bits);
+  if (rc) return rc;
+  if (num_layers <= 0 || kv_heads <= 0) return fail(TQ_ERR_BAD_ARG, "num_layers and kv_heads must be positive");
+  if (seq_new < 0 || offset < 0) return fail(TQ_ERR_BAD_ARG, "seq_new and offset must be non-negative");
+  if (offset + seq_new > capacity) return fail(TQ_ERR_BAD_ARG, "append past slab capacity");
+  if (seq_new == 0) return TQ_OK;
+  if (!keys || !values || !key_boundaries || !value_boundaries || !key_codes || !value_codes)
+    return fail(TQ_ERR_BAD_ARG, "null pointer argument");
+  if ((flags & (TQ_ROTATE_KEYS | TQ_ROTATE_VALUES)) && (!signs_left || !signs_right))
+    return fail(TQ_ERR_BAD_ARG, "rotation flags need signs_left and signs_right");
+  if (dtype != TQ_F32 && dtype != TQ_F16) return fail(TQ_ERR_BAD_ARG, "dtype must be F32 or F16");
+  AppendParams p{};
+  p.keys = keys;
+  p.values = values;
+  p.dtype = dtype;
+  p.rows = static_cast<int64_t>(num_layers) * kv_heads * seq_new;
+  p.streams = 2;
+  p.seq_new = seq_new;
+  p.rotate_keys = (flags & TQ_ROTATE_KEYS) != 0;
+  p.rotate_values = (flags & TQ_ROTATE_VALUES) != 0;
+  p.signs_left = signs_left;
+  p.signs_right = signs_right;
+  p.key_bnd = key_boundaries;
+  p.value_bnd = value_boundaries;
+  p.key_codes = key_codes;
+  p.value_codes = value_codes;
+  p.capacity = capacity;
+  p.offset = offset;
+  p.scaled = key_scales != nullptr;
+  p.key_scales = key_scales;
+  p.value_scales = value_scales;
+  return with_d<AppendBody>(head_dim, p, bits, stream);
+}
+
+int qdq_impl(const void* keys, const void* values, int dtype, int64_t rows, int head_dim, int bits,
+             const float* signs_left, const float* signs_right, int flags, const float* key_boundaries,
+             const float* value_boundaries, const float* key_centroids, const float* value_centroids,
+             float* key_out, float* value_out, bool scaled, hipStream_t stream) {
+  int rc = check_geometry(head_dim, bits);
+  if (rc) return rc;
+  if (rows < 0) return fail(TQ_ERR_BAD_ARG, "rows must be non-negative");
+  if (rows == 0) return TQ_OK;
+  if (!keys || !key_boundaries || !key_centroids || !key_out) return fail(TQ_ERR_BAD_ARG, "null key argument");
+  const bool two = values != nullptr;
+  if (two && (!value_boundaries || !value_centroids || !value_out))
+    return fail(TQ_ERR_BAD_ARG, "null value argument");
+  if ((flags & (TQ_ROTATE_KEYS | TQ_ROTATE_VALUES)) && (!signs_left || !signs_right))
+    return fail(TQ_ERR_BAD_ARG, "rotation flags need signs_left and signs_right");
+  if (dtype != TQ_F32 && dtype != TQ_F16) return fail(TQ_ERR_BAD_ARG, "dtype must be F32 or F16");
+  AppendParams p{};
+  p.keys = keys;
+  p.values = two ? values : keys;
+  p.dtype = dtype;
+  p.rows = rows;
+  p.streams = two ? 2 : 1;
+  p.seq_new = rows;
+  p.rotate_keys = (flags & TQ_ROTATE_KEYS) != 0;
+  p.rotate_values = (flags & TQ_ROTATE_VALUES) != 0;
+  p.signs_left = signs_left;
+  p.signs_right = signs_right;
+  p.key_bnd = key_boundaries;
+  p.value_bnd = two ? value_boundaries : key_boundaries;
+  p.key_cent = key_centroids;
+  p.value_cent = two ? value_centroids : key_centroids;
+  p.key_out = key_out;
+  p.value_out = two ? value_out : key_out;
+  p.dequant = true;
+  p.scaled = scaled;
+  return with_d<AppendBody>(head_dim, p, bits, stream);
+}
+
+int unpack_impl(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, int head_dim, int bits,
+                const float* centroids, const float* scales, float* out, hipStream_t stream) {
+  int rc = check_geometry(head_dim, bits);
+  if (rc) return rc;
+  if (groups < 0 || seq_len < 0 || capacity < seq_len) return fail(TQ_ERR_BAD_ARG, "bad unpack extents");
+  if (groups == 0 || seq_len == 0) return TQ_OK;
+  if (!codes || !centroids || !out) return fail(TQ_ERR_BAD_ARG, "null pointer argument");
+  return with_d<UnpackBody>(head_dim, codes, groups, capacity, seq_len, bits, centroids, scales, out, stream);
+}
 
 }  // namespace
 
@@ -1657,35 +1828,21 @@ int tq_append(const void* keys, const void* values, int dtype, int num_layers, i
               int head_dim, int bits, const float* signs_left, const float* signs_right, int flags,
               const float* key_boundaries, const float* value_boundaries, uint32_t* key_codes,
               uint32_t* value_codes, int64_t capacity, int64_t offset, hipStream_t stream) {
-  int rc = check_geometry(head_dim, bits);
-  if (rc) return rc;
-  if (num_layers <= 0 || kv_heads <= 0) return fail(TQ_ERR_BAD_ARG, "num_layers and kv_heads must be positive");
-  if (seq_new < 0 || offset < 0) return fail(TQ_ERR_BAD_ARG, "seq_new and offset must be non-negative");
-  if (offset + seq_new > capacity) return fail(TQ_ERR_BAD_ARG, "append past slab capacity");
-  if (seq_new == 0) return TQ_OK;
-  if (!keys || !values || !key_boundaries || !value_boundaries || !key_codes || !value_codes)
-    return fail(TQ_ERR_BAD_ARG, "null pointer argument");
-  if ((flags & (TQ_ROTATE_KEYS | TQ_ROTATE_VALUES)) && (!signs_left || !signs_right))
-    return fail(TQ_ERR_BAD_ARG, "rotation flags need signs_left and signs_right");
-  if (dtype != TQ_F32 && dtype != TQ_F16) return fail(TQ_ERR_BAD_ARG, "dtype must be F32 or F16");
-  AppendParams p{};
-  p.keys = keys;
-  p.values = values;
-  p.dtype = dtype;
-  p.rows = static_cast<int64_t>(num_layers) * kv_heads * seq_new;
-  p.streams = 2;
-  p.seq_new = seq_new;
-  p.rotate_keys = (flags & TQ_ROTATE_KEYS) != 0;
-  p.rotate_values = (flags & TQ_ROTATE_VALUES) != 0;
-  p.signs_left = signs_left;
-  p.signs_right = signs_right;
-  p.key_bnd = key_boundaries;
-  p.value_bnd = value_boundaries;
-  p.key_codes = key_codes;
-  p.value_codes = value_codes;
-  p.capacity = capacity;
-  p.offset = offset;
-  return with_d<AppendBody>(head_dim, p, bits, stream);
+  return append_impl(keys, values, dtype, num_layers, kv_heads, seq_new, head_dim, bits, signs_left, signs_right, flags,
+                     key_boundaries, value_boundaries, key_codes, value_codes, capacity, offset, nullptr, nullptr,
+                     stream);
+}
+
+int tq_append_scaled(const void* keys, const void* values, int dtype, int num_layers, int kv_heads, int64_t seq_new,
+                     int head_dim, int bits, const float* signs_left, const float* signs_right, int flags,
+                     const float* key_boundaries, const float* value_boundaries, uint32_t* key_codes,
+                     uint32_t* value_codes, float* key_scales, float* value_scales, int64_t capacity,
+                     int64_t offset, hipStream_t stream) {
+  if (key_scales == nullptr || value_scales == nullptr)
+    return fail(TQ_ERR_BAD_ARG, "key_scales and value_scales must be non-null");
+  return append_impl(keys, values, dtype, num_layers, kv_heads, seq_new, head_dim, bits, signs_left, signs_right, flags,
+                     key_boundaries, value_boundaries, key_codes, value_codes, capacity, offset, key_scales,
+                     value_scales, stream);
 }
 
 int tq_quantize_dequantize(const void* keys, const void* values, int dtype, int64_t rows, int head_dim, int bits,
@@ -1693,46 +1850,29 @@ int tq_quantize_dequantize(const void* keys, const void* values, int dtype, int6
                            const float* key_boundaries, const float* value_boundaries,
                            const float* key_centroids, const float* value_centroids, float* key_out,
                            float* value_out, hipStream_t stream) {
-  int rc = check_geometry(head_dim, bits);
-  if (rc) return rc;
-  if (rows < 0) return fail(TQ_ERR_BAD_ARG, "rows must be non-negative");
-  if (rows == 0) return TQ_OK;
-  if (!keys || !key_boundaries || !key_centroids || !key_out) return fail(TQ_ERR_BAD_ARG, "null key argument");
-  const bool two = values != nullptr;
-  if (two && (!value_boundaries || !value_centroids || !value_out))
-    return fail(TQ_ERR_BAD_ARG, "null value argument");
-  if ((flags & (TQ_ROTATE_KEYS | TQ_ROTATE_VALUES)) && (!signs_left || !signs_right))
-    return fail(TQ_ERR_BAD_ARG, "rotation flags need signs_left and signs_right");
-  if (dtype != TQ_F32 && dtype != TQ_F16) return fail(TQ_ERR_BAD_ARG, "dtype must be F32 or F16");
-  AppendParams p{};
-  p.keys = keys;
-  p.values = two ? values : keys;
-  p.dtype = dtype;
-  p.rows = rows;
-  p.streams = two ? 2 : 1;
-  p.seq_new = rows;
-  p.rotate_keys = (flags & TQ_ROTATE_KEYS) != 0;
-  p.rotate_values = (flags & TQ_ROTATE_VALUES) != 0;
-  p.signs_left = signs_left;
-  p.signs_right = signs_right;
-  p.key_bnd = key_boundaries;
-  p.value_bnd = two ? value_boundaries : key_boundaries;
-  p.key_cent = key_centroids;
-  p.value_cent = two ? value_centroids : key_centroids;
-  p.key_out = key_out;
-  p.value_out = two ? value_out : key_out;
-  p.dequant = true;
-  return with_d<AppendBody>(head_dim, p, bits, stream);
+  return qdq_impl(keys, values, dtype, rows, head_dim, bits, signs_left, signs_right, flags, key_boundaries,
+                  value_boundaries, key_centroids, value_centroids, key_out, value_out, false, stream);
+}
+
+int tq_quantize_dequantize_scaled(const void* keys, const void* values, int dtype, int64_t rows, int head_dim,
+                                  int bits, const float* signs_left, const float* signs_right, int flags,
+                                  const float* key_boundaries, const float* value_boundaries,
+                                  const float* key_centroids, const float* value_centroids, float* key_out,
+                                  float* value_out, hipStream_t stream) {
+  return qdq_impl(keys, values, dtype, rows, head_dim, bits, signs_left, signs_right, flags, key_boundaries,
+                  value_boundaries, key_centroids, value_centroids, key_out, value_out, true, stream);
 }
 
 int tq_unpack_dequantize(const uint32_t* codes, int64_t groups, int64_t capacity, int64_t seq_len, int head_dim,
                          int bits, const float* centroids, float* out, hipStream_t stream) {
-  int rc = check_geometry(head_dim, bits);
-  if (rc) return rc;
-  if (groups < 0 || seq_len < 0 || capacity < seq_len) return fail(TQ_ERR_BAD_ARG, "bad unpack extents");
-  if (groups == 0 || seq_len == 0) return TQ_OK;
-  if (!codes || !centroids || !out) return fail(TQ_ERR_BAD_ARG, "null pointer argument");
-  return with_d<UnpackBody>(head_dim, codes, groups, capacity, seq_len, bits, centroids, out, stream);
+  return unpack_impl(codes, groups, capacity, seq_len, head_dim, bits, centroids, nullptr, out, stream);
+}
+
+int tq_unpack_dequantize_scaled(const uint32_t* codes, const float* scales, int64_t groups, int64_t capacity,
+                                int64_t seq_len, int head_dim, int bits, const float* centroids, float* out,
+                                hipStream_t stream) {
+  if (scales == nullptr) return fail(TQ_ERR_BAD_ARG, "scales must be non-null");
+  return unpack_impl(codes, groups, capacity, seq_len, head_dim, bits, centroids, scales, out, stream);
 }
 
 int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int head_dim, int64_t seq_len,
@@ -1769,6 +1909,21 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
   return tq_decode_timed(query, query_dtype, num_layers, query_heads, kv_heads, head_dim, bits, key_codes,
                          value_codes, capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right,
                          flags, current_keys, current_values, n_splits, workspace, out, stream, nullptr, nullptr);
+}
+
+int tq_decode_scaled(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads, int head_dim,
+                     int bits, const uint32_t* key_codes, const uint32_t* value_codes, const float* key_scales,
+                     const float* value_scales, int64_t capacity, int64_t seq_len, const float* key_centroids,
+                     const float* value_centroids, const float* signs_left, const float* signs_right, int flags,
+                     const float* current_keys, const float* current_values, int n_splits, void* workspace,
+                     float* out, hipStream_t stream) {
+  if (!valid_bits(bits)) return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
+  if (seq_len > 0 && (key_scales == nullptr || value_scales == nullptr))
+    return fail(TQ_ERR_BAD_ARG, "key_scales and value_scales must be non-null");
+  return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes, value_codes,
+                       capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, flags,
+                       current_keys, current_values, n_splits, workspace, out, stream, nullptr, nullptr, nullptr,
+                       seq_len > 0 ? key_scales : nullptr, seq_len > 0 ? value_scales : nullptr);
 }
 
 int tq_decode_append(const void* query, const void* new_keys, const void* new_values, int dtype, int num_layers,

@@ -45,13 +45,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tq_fwht": (_i, [_p, _i, _p, _i64, _i, _p, _p, _i, _p]),
     "tq_quantize_pack": (_i, [_p, _i64, _i, _i, _p, _p, _p]),
     "tq_append": (_i, [_p, _p, _i, _i, _i, _i64, _i, _i, _p, _p, _i, _p, _p, _p, _p, _i64, _i64, _p]),
+    "tq_append_scaled": (_i, [_p, _p, _i, _i, _i, _i64, _i, _i, _p, _p, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p]),
     "tq_quantize_dequantize": (_i, [_p, _p, _i, _i64, _i, _i, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p]),
+    "tq_quantize_dequantize_scaled": (_i, [_p, _p, _i, _i64, _i, _i, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p]),
     "tq_unpack_dequantize": (_i, [_p, _i64, _i64, _i64, _i, _i, _p, _p, _p]),
+    "tq_unpack_dequantize_scaled": (_i, [_p, _p, _i64, _i64, _i64, _i, _i, _p, _p, _p]),
     "tq_decode_default_splits": (_i, [_i, _i, _i, _i, _i64, _i]),
     "tq_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "tq_decode": (
         _i,
         [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _p],
+    ),
+    "tq_decode_scaled": (
+        _i,
+        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _p],
     ),
     "tq_decode_timed": (
         _i,

@@ -3,7 +3,9 @@
 Packed codes live in two int32 tensors (the uint32 bit patterns) of shape
 [L, Hkv, capacity, W] -- the reference's canonical layout
 (docs/contracts/packed-kv-layout.md:5-10, cache_mlx.py:105-109).  Capacity
-grows geometrically like cache_mlx.py:353-371.
+grows geometrically like cache_mlx.py:353-371.  With ``scale_mode="rms"`` two
+float32 scale slabs [L, Hkv, capacity] sit beside them (one per-vector scale
+per token and stream) and every kernel call takes its ``_scaled`` form.
 """
 
 from __future__ import annotations
@@ -40,6 +42,9 @@ class SlabStore:
         shape = (config.num_layers, config.kv_heads, initial_capacity, self.layout.packed_words)
         self.key_codes = torch.zeros(shape, dtype=torch.int32, device=dev)
         self.value_codes = torch.zeros_like(self.key_codes)
+        self.scaled = config.scale_mode == "rms"
+        self.key_scales = torch.zeros(shape[:3], dtype=torch.float32, device=dev) if self.scaled else None
+        self.value_scales = torch.zeros(shape[:3], dtype=torch.float32, device=dev) if self.scaled else None
         self.key_centroids = torch.from_numpy(key_codebook.centroids.copy()).to(dev)
         self.value_centroids = torch.from_numpy(value_codebook.centroids.copy()).to(dev)
         self.key_boundaries = torch.from_numpy(codebook_boundaries(key_codebook)).to(dev)
@@ -61,12 +66,21 @@ class SlabStore:
         new_k[:, :, : self.length].copy_(self.key_codes[:, :, : self.length])
         new_v[:, :, : self.length].copy_(self.value_codes[:, :, : self.length])
         self.key_codes, self.value_codes = new_k, new_v
+        if self.scaled:
+            new_ks = torch.zeros(shape[:3], dtype=torch.float32, device=self.device)
+            new_vs = torch.zeros_like(new_ks)
+            new_ks[:, :, : self.length].copy_(self.key_scales[:, :, : self.length])
+            new_vs[:, :, : self.length].copy_(self.value_scales[:, :, : self.length])
+            self.key_scales, self.value_scales = new_ks, new_vs
         self.capacity = new_capacity
 
     def reset(self) -> None:
         self.length = 0
         self.key_codes.zero_()
         self.value_codes.zero_()
+        if self.scaled:
+            self.key_scales.zero_()
+            self.value_scales.zero_()
 
     # -------------------------------------------------------------- kernels
 
@@ -80,8 +94,9 @@ class SlabStore:
         self.ensure_capacity(self.length + seq_new)
         flags = (_lib.TQ_ROTATE_KEYS if rotate_keys else 0) | (_lib.TQ_ROTATE_VALUES if rotate_values else 0)
         cfg = self.config
+        scale_args = (self.key_scales.data_ptr(), self.value_scales.data_ptr()) if self.scaled else ()
         _lib.call(
-            "tq_append",
+            "tq_append_scaled" if self.scaled else "tq_append",
             keys.data_ptr(),
             values.data_ptr(),
             dtype_code(keys),
@@ -97,6 +112,7 @@ class SlabStore:
             self.value_boundaries.data_ptr(),
             self.key_codes.data_ptr(),
             self.value_codes.data_ptr(),
+            *scale_args,
             self.capacity,
             self.length,
             stream_handle(self.device),
@@ -115,7 +131,7 @@ class SlabStore:
         v_out = torch.empty_like(k_out)
         flags = (_lib.TQ_ROTATE_KEYS if rotate_keys else 0) | (_lib.TQ_ROTATE_VALUES if rotate_values else 0)
         _lib.call(
-            "tq_quantize_dequantize",
+            "tq_quantize_dequantize_scaled" if self.scaled else "tq_quantize_dequantize",
             keys.data_ptr(),
             values.data_ptr(),
             dtype_code(keys),
@@ -166,6 +182,8 @@ class SlabStore:
             current_keys=None if current is None else current[0],
             current_values=None if current is None else current[1],
             n_splits=n_splits,
+            key_scales=self.key_scales,
+            value_scales=self.value_scales,
         )
 
     def decode_append(
@@ -180,7 +198,17 @@ class SlabStore:
         rotate_values: bool,
         n_splits: int | None = None,
     ) -> torch.Tensor:
-        """Append one token (keys/values [L, Hkv, 1, D]) and decode with it: one launch."""
+        """Append one token (keys/values [L, Hkv, 1, D]) and decode with it: one launch.
+
+        Scaled slabs take three launches (dequantize the token, decode with it,
+        append it): the fused launch packs codes but writes no scales.
+        """
+        if self.scaled:
+            current = self.quantize_current(keys, values, rotate_keys=rotate_keys, rotate_values=rotate_values)
+            out = self.decode(queries, rotate_query=rotate_query, inverse_output=inverse_output, current=current,
+                              n_splits=n_splits)
+            self.append(keys, values, rotate_keys=rotate_keys, rotate_values=rotate_values)
+            return out
         cfg = self.config
         self.ensure_capacity(self.length + 1)
         dtype = queries.dtype
@@ -221,13 +249,15 @@ class SlabStore:
         shape = (cfg.num_layers, cfg.kv_heads, self.length, cfg.head_dim)
         keys = torch.zeros(shape, dtype=torch.float32, device=self.device)
         values = torch.zeros_like(keys)
-        for codes, cent, out in (
-            (self.key_codes, self.key_centroids, keys),
-            (self.value_codes, self.value_centroids, values),
+        for codes, cent, scales, out in (
+            (self.key_codes, self.key_centroids, self.key_scales, keys),
+            (self.value_codes, self.value_centroids, self.value_scales, values),
         ):
+            scale_args = (scales.data_ptr(),) if self.scaled else ()
             _lib.call(
-                "tq_unpack_dequantize",
+                "tq_unpack_dequantize_scaled" if self.scaled else "tq_unpack_dequantize",
                 codes.data_ptr(),
+                *scale_args,
                 groups,
                 self.capacity,
                 self.length,

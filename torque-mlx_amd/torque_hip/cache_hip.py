@@ -261,7 +261,8 @@ class TorqueKVCacheHIP:
 
     def _decode_packed(self, queries: torch.Tensor) -> torch.Tensor:
         profile = self.last_decode_profile if self.profile_decode_components else None
-        if profile is not None and self.resolve_decode_strategy() == "split_batched":
+        # The three-stage profile has no per-vector scales: scaled caches time the fused decode.
+        if profile is not None and self.resolve_decode_strategy() == "split_batched" and not self._store.scaled:
             return self._decode_staged(queries, profile)
         with EventTimer(profile, "packed_decode_seconds", self._store.device):
             return self._store.decode(

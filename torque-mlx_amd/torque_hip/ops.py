@@ -99,8 +99,14 @@ def packed_decode(
     current_values: torch.Tensor | None = None,
     n_splits: int | None = None,
     out: torch.Tensor | None = None,
+    key_scales: torch.Tensor | None = None,
+    value_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """One ``tq_decode`` launch on device tensors; returns out[L, Hq, D] float32."""
+    """One ``tq_decode`` launch on device tensors; returns out[L, Hq, D] float32.
+
+    With ``key_scales`` / ``value_scales`` ([L, Hkv, capacity] float32, slabs
+    written by ``tq_append_scaled``) the launch is ``tq_decode_scaled``.
+    """
     dev = query.device
     if n_splits is None or n_splits <= 0:
         n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev)
@@ -108,8 +114,12 @@ def packed_decode(
     if out is None:
         out = torch.empty((num_layers, query_heads, head_dim), dtype=torch.float32, device=dev)
     flags = (_lib.TQ_ROTATE_QUERY if rotate_query else 0) | (_lib.TQ_INVERSE_OUTPUT if inverse_output else 0)
+    scaled = key_scales is not None or value_scales is not None
+    if scaled and (key_scales is None or value_scales is None):
+        raise ValueError("key_scales and value_scales must both be given or both be None")
+    scale_args = (key_scales.data_ptr(), value_scales.data_ptr()) if scaled else ()
     _lib.call(
-        "tq_decode",
+        "tq_decode_scaled" if scaled else "tq_decode",
         query.data_ptr(),
         dtype_code(query),
         num_layers,
@@ -119,6 +129,7 @@ def packed_decode(
         bit_width,
         key_codes.data_ptr(),
         value_codes.data_ptr(),
+        *scale_args,
         capacity,
         seq_len,
         key_centroids.data_ptr(),
