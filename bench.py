@@ -110,7 +110,7 @@ def synthetic(seed, layers, kv_heads, query_heads, seq_len, head_dim, std):
     return q.astype(np.float16), k.astype(np.float16), v.astype(np.float16)
 
 
-def cpu_baseline(q, k_codes, v_codes, cache, head_subset: int, budget_s: float, gpu_out):
+def cpu_baseline(q, k_codes, v_codes, cache, head_subset: int, budget_s: float, gpu_out, k_scales=None, v_scales=None):
     """Time the CPU oracle (vectorised numpy restatement of cache.py:98-140) on a bounded sample.
 
     Sample: the first `head_subset` KV heads (and their query heads) at the full
@@ -123,6 +123,8 @@ def cpu_baseline(q, k_codes, v_codes, cache, head_subset: int, budget_s: float, 
     g = q.shape[1] // cfg.kv_heads
     qs = q[:, : head_subset * g].astype(np.float32)
     kc, vc = k_codes[:, :head_subset], v_codes[:, :head_subset]
+    ks = None if k_scales is None else k_scales[:, :head_subset]
+    vs = None if v_scales is None else v_scales[:, :head_subset]
     sl, sr = cache.rotation.signs_left, cache.rotation.signs_right
     kcent, vcent = cache.key_codebook.centroids, cache.value_codebook.centroids
 
@@ -130,7 +132,8 @@ def cpu_baseline(q, k_codes, v_codes, cache, head_subset: int, budget_s: float, 
         q_rot = o.rotation_apply(qs, sl, sr)[0]
         idx = np.arange(q_rot.shape[0]) // g
         out_rot = o.decode_packed_reference(
-            q_rot, kc[0][idx], vc[0][idx], kcent, vcent, bit_width=cfg.bit_width, head_dim=cfg.head_dim
+            q_rot, kc[0][idx], vc[0][idx], kcent, vcent, bit_width=cfg.bit_width, head_dim=cfg.head_dim,
+            key_scales=None if ks is None else ks[0][idx], value_scales=None if vs is None else vs[0][idx],
         )
         return o.rotation_inverse(out_rot, sl, sr)
 
@@ -426,6 +429,8 @@ def main() -> int:
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--splits", type=int, default=0, help="split count (0 = library default)")
+    ap.add_argument("--scale-mode", default="none", choices=["none", "rms"],
+                    help="per-vector scales of the cache (single-step workloads; 'none' is the reference format)")
     ap.add_argument(
         "--calibration-copy-mib",
         type=int,
@@ -459,19 +464,20 @@ def main() -> int:
     L, hkv, hq, d, bits, s, std, desc = WORKLOADS[args.workload]
     log(f"workload {desc}")
     q_np, k_np, v_np = synthetic(args.seed, L, hkv, hq, s, d, std)
-    cfg = th.TorqueConfig(bit_width=bits, head_dim=d, num_layers=L, kv_heads=hkv, rotation_seed=args.seed)
+    scaled = args.scale_mode == "rms"
+    cfg = th.TorqueConfig(bit_width=bits, head_dim=d, num_layers=L, kv_heads=hkv, rotation_seed=args.seed,
+                          scale_mode=args.scale_mode)
     cache = th.TorqueKVCacheHIP(config=cfg, initial_capacity=s, decode_tail_capacity=0)
     cache.append_many(key=torch.from_numpy(k_np).to(dev), value=torch.from_numpy(v_np).to(dev))
     torch.cuda.synchronize()
     store = cache._store
     w = store.layout.packed_words
-    packed_bytes = L * hkv * s * 2 * w * 4
+    packed_bytes = L * hkv * s * 2 * (w * 4 + (4 if scaled else 0))  # codes (+ one float32 scale per vector)
     algo_bytes = packed_bytes + L * hq * d * (2 + 4)  # + fp16 query in, fp32 output
     n_rep = max(3, ceil(args.replica_mib * 2**20 / packed_bytes))
     log(f"packed K+V {packed_bytes / 2**20:.1f} MiB per step, {n_rep} replicas")
-    reps = [(store.key_codes, store.value_codes)] + [
-        (store.key_codes.clone(), store.value_codes.clone()) for _ in range(n_rep - 1)
-    ]
+    slabs = (store.key_codes, store.value_codes) + ((store.key_scales, store.value_scales) if scaled else ())
+    reps = [slabs] + [tuple(t.clone() for t in slabs) for _ in range(n_rep - 1)]
     queries = [torch.from_numpy(q_np).to(dev)] + [
         torch.randn((L, hq, d), generator=torch.Generator(device=dev).manual_seed(i), device=dev).half()
         for i in range(1, 4)
@@ -480,14 +486,14 @@ def main() -> int:
     ws = ops.workspace_for(L, hkv, hq, d, n_splits, dev)
     out = torch.empty((L, hq, d), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    fn = _lib.load().tq_decode_timed
+    fn = _lib.load().tq_decode_scaled_timed if scaled else _lib.load().tq_decode_timed
     flags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT
     call_args = []
     for i in range(n_rep):
-        kc, vc = reps[i]
         qt = queries[i % len(queries)]
+        slab_ptrs = tuple(t.data_ptr() for t in reps[i])  # key codes, value codes (, key scales, value scales)
         call_args.append(
-            (qt.data_ptr(), _lib.TQ_F16, L, hq, hkv, d, bits, kc.data_ptr(), vc.data_ptr(), store.capacity, s,
+            (qt.data_ptr(), _lib.TQ_F16, L, hq, hkv, d, bits, *slab_ptrs, store.capacity, s,
              store.key_centroids.data_ptr(), store.value_centroids.data_ptr(), store.signs_left.data_ptr(),
              store.signs_right.data_ptr(), flags, None, None, n_splits, ws.data_ptr(), out.data_ptr(), stream)
         )
@@ -525,7 +531,7 @@ def main() -> int:
     kern_us = float(np.mean(kern_ms) * 1e3)
     kern_med_us = float(np.median(kern_ms) * 1e3)
     achieved = algo_bytes / (kern_us * 1e-6) / 1e9
-    kernel_name = f"decode_kernel<PackedB{bits},{d},4>"
+    kernel_name = f"decode_kernel<PackedB{bits},{d},4{',scaled' if scaled else ''}>"
     traffic, traffic_src = measured_traffic(kernel_name, args.workload)
     log(f"decode kernel mean {kern_us:.2f} us (median {kern_med_us:.2f}), wall {ms_per_step * 1e3:.2f} us/step")
 
@@ -553,6 +559,7 @@ def main() -> int:
             "query_dtype": "f16",
             "n_splits": n_splits,
             "slab_replicas": n_rep,
+            "scale_mode": args.scale_mode,
         },
         "kernel_us_per_step": round(kern_us, 3),
         "kernel_us_median": round(kern_med_us, 3),
@@ -622,7 +629,9 @@ def main() -> int:
         kc_np = store.key_codes[:, :, :s].cpu().numpy().view(np.uint32)
         vc_np = store.value_codes[:, :, :s].cpu().numpy().view(np.uint32)
         subset = 1 if s * d > 2**23 else hkv
-        per_step, n, err, rel = cpu_baseline(q_np, kc_np, vc_np, cache, subset, args.cpu_budget, gpu_out0)
+        ks_np = store.key_scales[:, :, :s].cpu().numpy() if scaled else None
+        vs_np = store.value_scales[:, :, :s].cpu().numpy() if scaled else None
+        per_step, n, err, rel = cpu_baseline(q_np, kc_np, vc_np, cache, subset, args.cpu_budget, gpu_out0, ks_np, vs_np)
         result["cpu_baseline"] = {
             "value": round(packed_bytes / per_step / 1e9, 4),
             "unit": "GB/s",

@@ -157,6 +157,16 @@ int tq_decode_scaled(const void* query, int query_dtype, int num_layers, int que
                      const float* current_keys, const float* current_values, int n_splits, void* workspace,
                      float* out, hipStream_t stream);
 
+/* tq_decode_scaled with HIP events bound to the split kernel's launch
+ * (start/stop may be NULL), as tq_decode_timed. */
+int tq_decode_scaled_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
+                           int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
+                           const float* key_scales, const float* value_scales, int64_t capacity, int64_t seq_len,
+                           const float* key_centroids, const float* value_centroids, const float* signs_left,
+                           const float* signs_right, int flags, const float* current_keys,
+                           const float* current_values, int n_splits, void* workspace, float* out,
+                           hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+
 /* Append one token to the packed slabs and decode with it in one launch:
  * the same as tq_append(new token at row seq_len) followed by
  * tq_decode(seq_len + 1) -- the packed words are identical and the output

@@ -357,14 +357,22 @@ def decode_packed_reference(
     *,
     bit_width: int,
     head_dim: int,
+    key_scales: np.ndarray | None = None,
+    value_scales: np.ndarray | None = None,
 ) -> np.ndarray:
     """Packed decode on already-rotated queries: q[B, D], codes[B, S, W] -> out_rot[B, D].
 
     Restates mlx_ops.py:571-595 (and the single-head K5 at mlx_ops.py:181-253):
-    unpack, centroid gather, softmax(q.k / sqrt(D)), weighted value sum.
+    unpack, centroid gather, softmax(q.k / sqrt(D)), weighted value sum.  With
+    per-vector scales [B, S] (the extension, see ``rms_scales``) each token is
+    centroid x scale.
     """
-    keys = dequantize(unpack_indices_batched(k_codes, bit_width, head_dim), key_centroids)
-    values = dequantize(unpack_indices_batched(v_codes, bit_width, head_dim), value_centroids)
+    kidx = unpack_indices_batched(k_codes, bit_width, head_dim)
+    vidx = unpack_indices_batched(v_codes, bit_width, head_dim)
+    keys = dequantize(kidx, key_centroids) if key_scales is None else dequantize_scaled(kidx, key_centroids, key_scales)
+    values = (
+        dequantize(vidx, value_centroids) if value_scales is None else dequantize_scaled(vidx, value_centroids, value_scales)
+    )
     return attention_decode_dense(query_rot, keys, values)
 
 

@@ -1917,12 +1917,25 @@ int tq_decode_scaled(const void* query, int query_dtype, int num_layers, int que
                      const float* value_centroids, const float* signs_left, const float* signs_right, int flags,
                      const float* current_keys, const float* current_values, int n_splits, void* workspace,
                      float* out, hipStream_t stream) {
+  return tq_decode_scaled_timed(query, query_dtype, num_layers, query_heads, kv_heads, head_dim, bits, key_codes,
+                                value_codes, key_scales, value_scales, capacity, seq_len, key_centroids,
+                                value_centroids, signs_left, signs_right, flags, current_keys, current_values,
+                                n_splits, workspace, out, stream, nullptr, nullptr);
+}
+
+int tq_decode_scaled_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
+                           int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
+                           const float* key_scales, const float* value_scales, int64_t capacity, int64_t seq_len,
+                           const float* key_centroids, const float* value_centroids, const float* signs_left,
+                           const float* signs_right, int flags, const float* current_keys,
+                           const float* current_values, int n_splits, void* workspace, float* out,
+                           hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (!valid_bits(bits)) return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
   if (seq_len > 0 && (key_scales == nullptr || value_scales == nullptr))
     return fail(TQ_ERR_BAD_ARG, "key_scales and value_scales must be non-null");
   return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes, value_codes,
                        capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, flags,
-                       current_keys, current_values, n_splits, workspace, out, stream, nullptr, nullptr, nullptr,
+                       current_keys, current_values, n_splits, workspace, out, stream, start, stop, nullptr,
                        seq_len > 0 ? key_scales : nullptr, seq_len > 0 ? value_scales : nullptr);
 }
 
