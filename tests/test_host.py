@@ -19,9 +19,22 @@ def test_config_validation_and_variant():
     assert th.TorqueConfig(bit_width=3, head_dim=128, fused_weights=True).variant_id == "b3-h128-hadamard-fused"
     assert th.TorqueConfig().variant_id == "b4-h128-hadamard-unfused"
     for bad, msg in ((dict(bit_width=5), "Unsupported bit width"), (dict(head_dim=96), "Unsupported head dimension"),
-                     (dict(num_layers=0), "num_layers"), (dict(kv_heads=0), "kv_heads")):
+                     (dict(num_layers=0), "num_layers"), (dict(kv_heads=0), "kv_heads"),
+                     (dict(scale_mode="max"), "scale_mode")):
         with pytest.raises(ValueError, match=msg):
             th.TorqueConfig(**bad).validate()
+
+
+def test_scale_mode_config_and_manifest_fields():
+    """The per-vector scale extension: reference-format manifests carry no scale_mode field and load as "none";
+    "rms" round-trips and marks the variant id."""
+    from torque_hip.artifact import config_from_dict, config_to_dict
+
+    plain = th.TorqueConfig(bit_width=4, head_dim=128, kv_heads=8)
+    assert "scale_mode" not in config_to_dict(plain) and config_from_dict(config_to_dict(plain)) == plain
+    rms = th.TorqueConfig(bit_width=4, head_dim=128, kv_heads=8, scale_mode="rms")
+    assert config_to_dict(rms)["scale_mode"] == "rms" and config_from_dict(config_to_dict(rms)) == rms
+    assert rms.variant_id == "b4-h128-hadamard-unfused-rms"
 
 
 def test_layout():

@@ -52,11 +52,14 @@ def config_from_dict(payload: Mapping[str, object]) -> TorqueConfig:
         fused_weights=bool(payload["fused_weights"]),
         rotation_mode=RotationMode(str(payload["rotation_mode"])),
         rotation_seed=int(payload["rotation_seed"]),
+        scale_mode=str(payload.get("scale_mode", "none")),
     )
 
 
 def config_to_dict(config: TorqueConfig) -> dict[str, object]:
-    return {
+    """The reference's runtime_config fields; ``scale_mode`` (an extension) only when it is not "none", so
+    manifests of the reference format stay byte-identical."""
+    out: dict[str, object] = {
         "bit_width": config.bit_width,
         "head_dim": config.head_dim,
         "num_layers": config.num_layers,
@@ -65,6 +68,9 @@ def config_to_dict(config: TorqueConfig) -> dict[str, object]:
         "rotation_mode": RotationMode(config.rotation_mode).value,
         "rotation_seed": config.rotation_seed,
     }
+    if config.scale_mode != "none":
+        out["scale_mode"] = config.scale_mode
+    return out
 
 
 @dataclass(frozen=True)
