@@ -192,3 +192,31 @@ def test_rms_mode_tracks_unquantized_attention_better(hip_device):
         got = cache.decode(query=q).reshape(exact.shape)
         errs[mode] = float(np.linalg.norm(got - exact) / np.linalg.norm(exact))
     assert errs["rms"] < 0.5 * errs["none"], errs
+
+
+def test_rms_manifest_builds_scaled_cache(hip_device):
+    """A manifest whose runtime_config carries scale_mode "rms" survives JSON and builds a scaled
+    TorqueKVCache (the reference cache.py API) whose decode matches the oracle on its own contents."""
+    import json
+
+    import torque_hip as th
+    from torque_hip.artifact import TorqueArtifact, TorqueArtifactManifest
+
+    cfg = th.TorqueConfig(bit_width=3, head_dim=64, num_layers=2, kv_heads=2, fused_weights=True, rotation_seed=5,
+                          scale_mode="rms")
+    manifest = TorqueArtifactManifest(model_name="m", architecture="a", source_format="s", runtime_config=cfg,
+                                      key_codebook=th.build_gaussian_codebook(3, seed=5),
+                                      value_codebook=th.build_gaussian_codebook(3, seed=6))
+    manifest = TorqueArtifactManifest.from_dict(json.loads(json.dumps(manifest.to_dict())))
+    assert manifest.runtime_config.scale_mode == "rms"
+    cache = TorqueArtifact(manifest=manifest).build_cache()
+    assert isinstance(cache, th.TorqueKVCache) and cache.metadata.variant_id == "b3-h64-hadamard-fused-rms"
+    rng = np.random.default_rng(21)
+    for _ in range(30):
+        cache.append(key=_varied_rows(rng, (2, 2, 64)).astype(np.float32),
+                     value=_varied_rows(rng, (2, 2, 64)).astype(np.float32))
+    assert cache._store.scaled and bool((cache._store.key_scales[:, :, :30] > 0).all())
+    q = rng.normal(size=(2, 2, 64)).astype(np.float32)
+    got = cache.decode(query=q)
+    exp = _expected_decode(cache, q)
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * float(np.abs(exp).max()))
