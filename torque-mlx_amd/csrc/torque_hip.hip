@@ -988,7 +988,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 // rotated back, so every dimension is independent: one workgroup per (query
 // head, kMergeDims dimensions), its threads split the splits into kMergeGroups
 // strided groups and issue all their loads before the (max, sum) reduction.
-constexpr int kMergeDims = 32;
+constexpr int kMergeDims = 16;  // 16: M -0.6 us per step against 32 (8 equal, 64 +2 us)
 constexpr int kMergeGroups = kBlock / kMergeDims;
 constexpr int kMergePerThread = kMaxSplits / kMergeGroups;
 
