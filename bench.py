@@ -442,8 +442,9 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
-            "bench.py measures one GPU: the decode path shards by KV head or by sequence across GPUs "
-            "(see DESIGN.md), but this build runs and reports a single MI355X only.",
+            "bench.py measures one GPU: the decode path would shard by KV head (no exchange) or by sequence "
+            "(one all-gather of per-head (max, sum, accumulator) partials, then the same log-sum-exp merge) "
+            "across GPUs, but this build runs and reports a single MI355X only.",
             file=sys.stderr,
         )
         return 2
