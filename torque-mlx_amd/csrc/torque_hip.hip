@@ -1008,8 +1008,13 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(const MergeArgs a) {
   __shared__ float s_red[kWavesPerBlock];
   __shared__ float s_part[kMergeGroups][kMergeDims];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
-  const int64_t qhg = blockIdx.x / CH;
-  const int c = static_cast<int>(blockIdx.x - qhg * CH);
+  // Same XCD remap as the split kernel: XCD x takes the x-th eighth of the
+  // query heads, whose partials that kernel wrote through the same XCD's L2
+  // (measured: C5 loop 336 -> 332 us per step, M unchanged).
+  int64_t mb = blockIdx.x;
+  if ((gridDim.x & 7) == 0) mb = (mb & 7) * (gridDim.x >> 3) + (mb >> 3);
+  const int64_t qhg = mb / CH;
+  const int c = static_cast<int>(mb - qhg * CH);
   const int ns = a.n_splits;
   const int d = tid % kMergeDims, grp = tid / kMergeDims;
   const float* ml = a.ws_ml + qhg * ns * 2;
