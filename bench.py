@@ -238,11 +238,11 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
         fused_step, unfused_step = [], []
         for l, st in enumerate(stores):
             fused_step.append((lib.tq_decode_append, (
-                queries[t, l].data_ptr(), new_k[t, l].data_ptr(), new_v[t, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d,
-                bits, st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, seq,
+                queries[t, l].data_ptr(), _lib.TQ_F16, new_k[t, l].data_ptr(), new_v[t, l].data_ptr(), _lib.TQ_F16, 1,
+                hq, hkv, d, bits, st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, seq,
                 st.key_centroids.data_ptr(), st.value_centroids.data_ptr(), st.key_boundaries.data_ptr(),
-                st.value_boundaries.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), rot, dflags, args.splits,
-                ws.data_ptr(), out[l].data_ptr(), stream)))
+                st.value_boundaries.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), rot, dflags,
+                args.splits, ws.data_ptr(), ws.numel(), out[l].data_ptr(), stream)))
             unfused_step.append((lib.tq_append, (
                 new_k[t, l].data_ptr(), new_v[t, l].data_ptr(), _lib.TQ_F16, 1, hkv, 1, d, bits, st.signs_left.data_ptr(),
                 st.signs_right.data_ptr(), rot, st.key_boundaries.data_ptr(), st.value_boundaries.data_ptr(),
@@ -251,7 +251,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
                 queries[t, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d, bits, st.key_codes.data_ptr(),
                 st.value_codes.data_ptr(), st.capacity, seq + 1, st.key_centroids.data_ptr(),
                 st.value_centroids.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), dflags, None, None,
-                args.splits, ws.data_ptr(), out[l].data_ptr(), stream)))
+                args.splits, ws.data_ptr(), ws.numel(), out[l].data_ptr(), stream)))
         calls.append(fused_step)
         calls_unfused.append(unfused_step)
 
@@ -261,7 +261,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
             _lib.check(lib.tq_decode(queries[0, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d, bits, st.key_codes.data_ptr(),
                                      st.value_codes.data_ptr(), st.capacity, s0, st.key_centroids.data_ptr(),
                                      st.value_centroids.data_ptr(), st.signs_left.data_ptr(),
-                                     st.signs_right.data_ptr(), dflags, None, None, 0, ws.data_ptr(),
+                                     st.signs_right.data_ptr(), dflags, None, None, 0, ws.data_ptr(), ws.numel(),
                                      out[l].data_ptr(), stream))
     # a 1 GiB read between steps evicts the slabs from the 256 MB Infinity Cache; it is outside the events
     flush = torch.empty(2**30, dtype=torch.uint8, device=dev)
@@ -496,7 +496,8 @@ def main() -> int:
         call_args.append(
             (qt.data_ptr(), _lib.TQ_F16, L, hq, hkv, d, bits, *slab_ptrs, store.capacity, s,
              store.key_centroids.data_ptr(), store.value_centroids.data_ptr(), store.signs_left.data_ptr(),
-             store.signs_right.data_ptr(), flags, None, None, n_splits, ws.data_ptr(), out.data_ptr(), stream)
+             store.signs_right.data_ptr(), flags, None, None, n_splits, ws.data_ptr(), ws.numel(), out.data_ptr(),
+             stream)
         )
 
     def run(k_steps, events=None):
@@ -600,7 +601,8 @@ def main() -> int:
         dfn = _lib.load().tq_decode_dense_timed
         dargs = [
             (queries[i % len(queries)].data_ptr(), _lib.TQ_F16, dreps[i][0].data_ptr(), dreps[i][1].data_ptr(),
-             _lib.TQ_F16, L, hq, hkv, d, s, s, None, None, 0, n_splits, ws.data_ptr(), out.data_ptr(), stream)
+             _lib.TQ_F16, L, hq, hkv, d, s, s, None, None, 0, n_splits, ws.data_ptr(), ws.numel(), out.data_ptr(),
+             stream)
             for i in range(n_drep)
         ]
         for i in range(args.warmup):

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TQ_ABI_VERSION 1
+#define TQ_ABI_VERSION 2
 
 enum {
   TQ_OK = 0,
@@ -125,7 +125,10 @@ int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int 
  * (n_splits <= 0: enough for the default split count on any sequence length
  * with num_cus compute units).  The workspace holds per-split partial results
  * between the two launches of one call; it needs no initialisation.  Calls
- * that share one workspace must be ordered (same stream). */
+ * that share one workspace must be ordered (same stream).  Every decode entry
+ * point takes the workspace's size in bytes (workspace_bytes) and returns
+ * TQ_ERR_BAD_ARG, before any launch, when it is smaller than the split plan
+ * the call resolves to needs. */
 size_t tq_decode_workspace_bytes(int num_layers, int kv_heads, int query_heads, int head_dim, int n_splits,
                                  int num_cus);
 
@@ -143,7 +146,8 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
               int bits, const uint32_t* key_codes, const uint32_t* value_codes, int64_t capacity,
               int64_t seq_len, const float* key_centroids, const float* value_centroids,
               const float* signs_left, const float* signs_right, int flags, const float* current_keys,
-              const float* current_values, int n_splits, void* workspace, float* out, hipStream_t stream);
+              const float* current_values, int n_splits, void* workspace, size_t workspace_bytes, float* out,
+              hipStream_t stream);
 
 /* tq_decode over slabs written by tq_append_scaled: a token's score is
  * multiplied by its key scale and its value by its value scale (scales
@@ -155,7 +159,7 @@ int tq_decode_scaled(const void* query, int query_dtype, int num_layers, int que
                      const float* value_scales, int64_t capacity, int64_t seq_len, const float* key_centroids,
                      const float* value_centroids, const float* signs_left, const float* signs_right, int flags,
                      const float* current_keys, const float* current_values, int n_splits, void* workspace,
-                     float* out, hipStream_t stream);
+                     size_t workspace_bytes, float* out, hipStream_t stream);
 
 /* tq_decode_scaled with HIP events bound to the split kernel's launch
  * (start/stop may be NULL), as tq_decode_timed. */
@@ -164,8 +168,8 @@ int tq_decode_scaled_timed(const void* query, int query_dtype, int num_layers, i
                            const float* key_scales, const float* value_scales, int64_t capacity, int64_t seq_len,
                            const float* key_centroids, const float* value_centroids, const float* signs_left,
                            const float* signs_right, int flags, const float* current_keys,
-                           const float* current_values, int n_splits, void* workspace, float* out,
-                           hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+                           const float* current_values, int n_splits, void* workspace, size_t workspace_bytes,
+                           float* out, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 /* Append one token to the packed slabs and decode with it in one launch:
  * the same as tq_append(new token at row seq_len) followed by
@@ -173,18 +177,20 @@ int tq_decode_scaled_timed(const void* query, int query_dtype, int num_layers, i
  * matches to float rounding -- but the new token's codes are produced inside
  * the decode's split-0 workgroups and the token joins the softmax from
  * registers, saving the append launch of every decode step.  new_keys /
- * new_values are [L, Hkv, D] in `dtype` (also the query dtype); append_flags
+ * new_values are [L, Hkv, D] in kv_dtype (TQ_F32 or TQ_F16, independent of
+ * the query's query_dtype; the token is quantized from its own values, as
+ * the reference quantizes float32 K/V, cache_mlx.py:442-466); append_flags
  * TQ_ROTATE_KEYS / TQ_ROTATE_VALUES as for tq_append, decode_flags as for
  * tq_decode.  seq_len (tokens already in the slabs) must be below capacity.
  * Replaces the per-layer decode_mlx_with_current + append pair of the
  * reference's Qwen decode step (qwen_mlx.py:826-828; cache_mlx.py:236-302,
  * 151-171). */
-int tq_decode_append(const void* query, const void* new_keys, const void* new_values, int dtype, int num_layers,
-                     int query_heads, int kv_heads, int head_dim, int bits, uint32_t* key_codes,
+int tq_decode_append(const void* query, int query_dtype, const void* new_keys, const void* new_values, int kv_dtype,
+                     int num_layers, int query_heads, int kv_heads, int head_dim, int bits, uint32_t* key_codes,
                      uint32_t* value_codes, int64_t capacity, int64_t seq_len, const float* key_centroids,
                      const float* value_centroids, const float* key_boundaries, const float* value_boundaries,
                      const float* signs_left, const float* signs_right, int append_flags, int decode_flags,
-                     int n_splits, void* workspace, float* out, hipStream_t stream);
+                     int n_splits, void* workspace, size_t workspace_bytes, float* out, hipStream_t stream);
 
 /* Same as tq_decode; start/stop events (may be NULL) are bound to the split
  * kernel itself, so hipEventElapsedTime gives its execution time (the merge
@@ -193,8 +199,8 @@ int tq_decode_timed(const void* query, int query_dtype, int num_layers, int quer
                     int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
                     int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,
                     const float* signs_left, const float* signs_right, int flags, const float* current_keys,
-                    const float* current_values, int n_splits, void* workspace, float* out, hipStream_t stream,
-                    hipEvent_t start, hipEvent_t stop);
+                    const float* current_values, int n_splits, void* workspace, size_t workspace_bytes, float* out,
+                    hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 /* Dense-KV decode attention with the same split-K structure, for float16 or
  * float32 K/V slabs [L, Hkv, capacity, D].  With kv_dtype TQ_F16 this is the
@@ -205,13 +211,13 @@ int tq_decode_timed(const void* query, int query_dtype, int num_layers, int quer
 int tq_decode_dense(const void* query, int query_dtype, const void* keys, const void* values, int kv_dtype,
                     int num_layers, int query_heads, int kv_heads, int head_dim, int64_t capacity, int64_t seq_len,
                     const float* signs_left, const float* signs_right, int flags, int n_splits, void* workspace,
-                    float* out, hipStream_t stream);
+                    size_t workspace_bytes, float* out, hipStream_t stream);
 
 int tq_decode_dense_timed(const void* query, int query_dtype, const void* keys, const void* values,
                           int kv_dtype, int num_layers, int query_heads, int kv_heads, int head_dim,
                           int64_t capacity, int64_t seq_len, const float* signs_left, const float* signs_right,
-                          int flags, int n_splits, void* workspace, float* out, hipStream_t stream,
-                          hipEvent_t start, hipEvent_t stop);
+                          int flags, int n_splits, void* workspace, size_t workspace_bytes, float* out,
+                          hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 /* Raw (unscaled) packed scores: query [B, D] (rotated), codes [B, S, W] -> scores [B, S].
  * Replaces score_packed_query_batched (mlx_ops.py:113-145, 501-531). */

@@ -45,7 +45,7 @@ def test_host_only_entry_points():
     from torque_hip import _lib
 
     lib = _lib.load()
-    assert lib.tq_abi_version() == 1
+    assert lib.tq_abi_version() == _lib.ABI_VERSION == 2
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 32768, 256) == 64
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 7, 256) == 1
     assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, 64, 256) > 64 * 8 * 4 * 128 * 4
@@ -69,7 +69,7 @@ def test_decode_argument_errors(args, code, message):
     p.update(args)
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     rc = lib.tq_decode(fake, 0, 1, p["query_heads"], 8, p["head_dim"], p["bits"], fake, fake, p["capacity"], 10,
-                       fake, fake, None, None, 0, None, None, 0, fake, fake, None)
+                       fake, fake, None, None, 0, None, None, 0, fake, 1 << 30, fake, None)
     assert rc == code
     assert message in lib.tq_last_error().decode()
 
@@ -87,9 +87,60 @@ def test_decode_launch_size_errors(num_layers, seq_len, n_splits, message):
     lib = _lib.load()
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     rc = lib.tq_decode(fake, 0, num_layers, 32, 8, 128, 4, fake, fake, seq_len, seq_len, fake, fake, None, None, 0,
-                       None, None, n_splits, fake, fake, None)
+                       None, None, n_splits, fake, 1 << 62, fake, None)
     assert rc == -1
     assert message in lib.tq_last_error().decode()
+
+
+def _decode_args(fake, n_splits, ws_bytes):
+    # tq_decode at the metric shape (1 layer, 32 query / 8 KV heads, D=128, 4-bit, 32K tokens)
+    return (fake, 0, 1, 32, 8, 128, 4, fake, fake, 32768, 32768, fake, fake, None, None, 0, None, None, n_splits, fake,
+            ws_bytes, fake, None)
+
+
+@pytest.mark.parametrize("n_splits", [1, 17, 64, 256])
+def test_decode_rejects_short_workspace(n_splits):
+    """A workspace sized below what the resolved split plan needs is refused before any launch."""
+    from torque_hip import _lib
+
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    need = lib.tq_decode_workspace_bytes(1, 8, 32, 128, n_splits, 256)
+    assert need > 0
+    rc = lib.tq_decode(*_decode_args(fake, n_splits, need - 1))
+    assert rc == -1
+    assert f"smaller than the {need} bytes this call needs ({n_splits} splits)" in lib.tq_last_error().decode()
+    # the same short workspace for the other decode entry points
+    rc = lib.tq_decode_dense(fake, 0, fake, fake, 1, 1, 32, 8, 128, 32768, 32768, None, None, 0, n_splits, fake,
+                             need - 1, fake, None)
+    assert rc == -1 and "bytes this call needs" in lib.tq_last_error().decode()
+    rc = lib.tq_decode_scaled(fake, 0, 1, 32, 8, 128, 4, fake, fake, fake, fake, 32768, 32768, fake, fake, None, None,
+                              0, None, None, n_splits, fake, need - 1, fake, None)
+    assert rc == -1 and "bytes this call needs" in lib.tq_last_error().decode()
+    rc = lib.tq_decode_append(fake, 0, fake, fake, 0, 1, 32, 8, 128, 4, fake, fake, 32769, 32768, fake, fake, fake,
+                              fake, fake, fake, 3, 3, n_splits, fake, need - 1, fake, None)
+    assert rc == -1 and "bytes this call needs" in lib.tq_last_error().decode()
+
+
+def test_workspace_query_covers_default_plan():
+    """n_splits <= 0 sizes the workspace for the default split count at any sequence length."""
+    from torque_hip import _lib
+
+    lib = _lib.load()
+    for seq_len in (1, 100, 4096, 32768, 1 << 20):
+        ns = lib.tq_decode_default_splits(1, 8, 32, 128, seq_len, 256)
+        assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, ns, 256) <= lib.tq_decode_workspace_bytes(1, 8, 32, 128, 0,
+                                                                                                        256)
+
+
+def test_decode_append_rejects_bad_kv_dtype():
+    from torque_hip import _lib
+
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    rc = lib.tq_decode_append(fake, 0, fake, fake, 7, 1, 32, 8, 128, 4, fake, fake, 32769, 32768, fake, fake, fake,
+                              fake, fake, fake, 3, 3, 0, fake, 1 << 30, fake, None)
+    assert rc == -1 and "new key/value dtype" in lib.tq_last_error().decode()
 
 
 def test_status_mapping():

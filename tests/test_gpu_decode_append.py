@@ -64,6 +64,51 @@ def test_decode_append_matches_append_then_decode(hip_device, bits, head_dim, la
         np.testing.assert_allclose(got, exp, atol=2e-6, rtol=1e-5, err_msg=f"step {step}")
 
 
+@pytest.mark.parametrize("q_dtype,kv_dtype", [(torch.float16, torch.float32), (torch.float32, torch.float16)])
+def test_decode_append_mixed_dtypes(hip_device, q_dtype, kv_dtype):
+    """The new token is quantized from its own values whatever the query's dtype (the reference quantizes
+    float32 K/V, cache_mlx.py:442-466): codes equal append()'s and the oracle's on float32 K/V, so an fp16
+    query never rounds fp32 keys before they are packed."""
+    gen = torch.Generator(device=hip_device).manual_seed(77)
+    a, b = _pair(4, 128, 1, 2, capacity=64)
+    model = o.OracleCache(bit_width=4, head_dim=128, num_layers=1, kv_heads=2,
+                          key_centroids=a.key_codebook.centroids, value_centroids=a.value_codebook.centroids,
+                          signs_left=a.rotation.signs_left, signs_right=a.rotation.signs_right)
+    for step in range(4):
+        q = torch.randn((1, 8, 128), generator=gen, device=hip_device).to(q_dtype)
+        k = (torch.randn((1, 2, 128), generator=gen, device=hip_device) * 3).to(kv_dtype)
+        v = (torch.randn((1, 2, 128), generator=gen, device=hip_device) * 3).to(kv_dtype)
+        got = a.decode_append(query=q, key=k, value=v, return_numpy=False).cpu().numpy()
+        b.append(key=k, value=v)
+        exp = b.decode(query=q, return_numpy=False).cpu().numpy()
+        model.append(k.float().cpu().numpy()[:, :, None], v.float().cpu().numpy()[:, :, None])
+        for x, y, m in zip(_codes(a), _codes(b), (model.k_codes, model.v_codes)):
+            np.testing.assert_array_equal(x, y)
+            np.testing.assert_array_equal(x.view(np.uint32), m)
+        np.testing.assert_allclose(got, exp, atol=2e-6, rtol=1e-5, err_msg=f"step {step}")
+        oracle_out = model.decode(q.float().cpu().numpy())[0]
+        np.testing.assert_allclose(got.reshape(oracle_out.shape), oracle_out, atol=2e-5, rtol=1e-4,
+                                   err_msg=f"step {step}")
+
+
+def test_mixed_kv_dtypes_quantize_at_float32(hip_device):
+    """append() and decode-with-current with an fp16 key and an fp32 value (or the reverse) quantize both at
+    float32: the codes equal those of the same token given as two float32 tensors."""
+    gen = torch.Generator(device=hip_device).manual_seed(78)
+    for kd, vd in ((torch.float16, torch.float32), (torch.float32, torch.float16)):
+        a, b = _pair(3, 64, 1, 2, capacity=16)
+        for _ in range(3):
+            k = (torch.randn((1, 2, 64), generator=gen, device=hip_device) * 2).to(kd)
+            v = (torch.randn((1, 2, 64), generator=gen, device=hip_device) * 2).to(vd)
+            a.append(key=k, value=v)
+            b.append(key=k.float(), value=v.float())
+        for x, y in zip(_codes(a), _codes(b)):
+            np.testing.assert_array_equal(x, y)
+        q = torch.randn((1, 8, 64), generator=gen, device=hip_device)
+        np.testing.assert_allclose(a.decode(query=q, return_numpy=False).cpu().numpy(),
+                                   b.decode(query=q, return_numpy=False).cpu().numpy(), atol=1e-6)
+
+
 def test_decode_append_against_oracle_and_split_counts(hip_device):
     import torque_hip as th
 
@@ -126,8 +171,8 @@ def test_decode_append_flags_growth_and_errors(hip_device):
     ws = torch.zeros(1 << 20, dtype=torch.uint8, device=hip_device)
     out = torch.empty((1, 4, 64), device=hip_device)
     with pytest.raises(ValueError, match="slab is full"):
-        _lib.call("tq_decode_append", q.data_ptr(), kv.data_ptr(), kv.data_ptr(), _lib.TQ_F32, 1, 4, 2, 64, 3,
-                  st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, st.capacity,
+        _lib.call("tq_decode_append", q.data_ptr(), _lib.TQ_F32, kv.data_ptr(), kv.data_ptr(), _lib.TQ_F32, 1, 4, 2,
+                  64, 3, st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, st.capacity,
                   st.key_centroids.data_ptr(), st.value_centroids.data_ptr(), st.key_boundaries.data_ptr(),
                   st.value_boundaries.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), 3, 3, 0,
-                  ws.data_ptr(), out.data_ptr(), None)
+                  ws.data_ptr(), ws.numel(), out.data_ptr(), None)

@@ -203,11 +203,13 @@ struct DecodeArgs {
   float sqrt_d;
   float q_scale;  // log2(e) / sqrt(D): scores come out in log2 units
   int rotate_query, inverse_output;
-  // Append mode (new_k != null): the token new_k/new_v [L, Hkv, D] (query
-  // dtype) is rotated, quantized and packed into the slabs at row seq_len by
-  // the split-0 workgroups, and joins the softmax as the current token.
+  // Append mode (new_k != null): the token new_k/new_v [L, Hkv, D] (float16
+  // when new_f16, else float32) is rotated, quantized and packed into the
+  // slabs at row seq_len by the split-0 workgroups, and joins the softmax as
+  // the current token.
   const void* new_k;
   const void* new_v;
+  int new_f16;
   const float* bnd_k;
   const float* bnd_v;
   uint32_t* k_slab;
@@ -456,7 +458,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     const void* src = wave == 0 ? a.new_k : a.new_v;
 #pragma unroll
     for (int i = 0; i < E; ++i)
-      tok[i] = QF16 ? __half2float(static_cast<const __half*>(src)[toff + i]) : static_cast<const float*>(src)[toff + i];
+      tok[i] = a.new_f16 ? __half2float(static_cast<const __half*>(src)[toff + i]) : static_cast<const float*>(src)[toff + i];
     const float* b = wave == 0 ? a.bnd_k : a.bnd_v;
 #pragma unroll
     for (int k = 0; k < kLevels; ++k) bnd[k] = b[k];
@@ -1319,6 +1321,7 @@ int dispatch_d(const DecodeArgs& a, int head_dim, int hg, int nblk, hipStream_t 
 struct AppendSpec {
   const void* keys;
   const void* values;
+  int dtype;  // TQ_F32 or TQ_F16
   const float* key_boundaries;
   const float* value_boundaries;
   int flags;  // TQ_ROTATE_KEYS | TQ_ROTATE_VALUES
@@ -1327,8 +1330,9 @@ struct AppendSpec {
 int decode_common(int fmt, const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
                   int head_dim, const void* keys, const void* values, int64_t capacity, int64_t seq_len,
                   const float* cent_k, const float* cent_v, const float* signs_left, const float* signs_right,
-                  int flags, const float* cur_k, const float* cur_v, int n_splits, void* workspace, float* out,
-                  hipStream_t stream, hipEvent_t start, hipEvent_t stop, const AppendSpec* app = nullptr,
+                  int flags, const float* cur_k, const float* cur_v, int n_splits, void* workspace,
+                  size_t workspace_bytes, float* out, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
+                  const AppendSpec* app = nullptr,
                   const float* k_scales = nullptr, const float* v_scales = nullptr) {
   int rc = check_geometry(head_dim, 0);
   if (rc) return rc;
@@ -1349,6 +1353,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
         app->value_boundaries == nullptr || keys == nullptr || values == nullptr)
       return fail(TQ_ERR_BAD_ARG, "new keys/values, boundaries and both slabs must be non-null");
     if (seq_len >= capacity) return fail(TQ_ERR_BAD_ARG, "slab is full: seq_len must be below capacity");
+    if (app->dtype != TQ_F32 && app->dtype != TQ_F16) return fail(TQ_ERR_BAD_ARG, "new key/value dtype must be F32 or F16");
     if ((app->flags & (TQ_ROTATE_KEYS | TQ_ROTATE_VALUES)) && (signs_left == nullptr || signs_right == nullptr))
       return fail(TQ_ERR_BAD_ARG, "rotation flags need signs_left and signs_right");
   }
@@ -1376,6 +1381,10 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const WsLayout wl = workspace_layout(static_cast<int64_t>(num_layers) * query_heads,
                                       static_cast<int64_t>(num_layers) * kv_heads, head_dim, p.n_splits);
+  if (workspace_bytes < wl.total)
+    return fail(TQ_ERR_BAD_ARG, "workspace of " + std::to_string(workspace_bytes) + " bytes is smaller than the " +
+                                    std::to_string(wl.total) + " bytes this call needs (" +
+                                    std::to_string(p.n_splits) + " splits)");
 
   DecodeArgs a{};
   a.q = query;
@@ -1404,6 +1413,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   if (app != nullptr) {
     a.new_k = app->keys;
     a.new_v = app->values;
+    a.new_f16 = app->dtype == TQ_F16;
     a.bnd_k = app->key_boundaries;
     a.bnd_v = app->value_boundaries;
     a.k_slab = const_cast<uint32_t*>(static_cast<const uint32_t*>(keys));
@@ -1910,10 +1920,11 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
               int bits, const uint32_t* key_codes, const uint32_t* value_codes, int64_t capacity, int64_t seq_len,
               const float* key_centroids, const float* value_centroids, const float* signs_left,
               const float* signs_right, int flags, const float* current_keys, const float* current_values,
-              int n_splits, void* workspace, float* out, hipStream_t stream) {
+              int n_splits, void* workspace, size_t workspace_bytes, float* out, hipStream_t stream) {
   return tq_decode_timed(query, query_dtype, num_layers, query_heads, kv_heads, head_dim, bits, key_codes,
                          value_codes, capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right,
-                         flags, current_keys, current_values, n_splits, workspace, out, stream, nullptr, nullptr);
+                         flags, current_keys, current_values, n_splits, workspace, workspace_bytes, out, stream,
+                         nullptr, nullptr);
 }
 
 int tq_decode_scaled(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads, int head_dim,
@@ -1921,11 +1932,11 @@ int tq_decode_scaled(const void* query, int query_dtype, int num_layers, int que
                      const float* value_scales, int64_t capacity, int64_t seq_len, const float* key_centroids,
                      const float* value_centroids, const float* signs_left, const float* signs_right, int flags,
                      const float* current_keys, const float* current_values, int n_splits, void* workspace,
-                     float* out, hipStream_t stream) {
+                     size_t workspace_bytes, float* out, hipStream_t stream) {
   return tq_decode_scaled_timed(query, query_dtype, num_layers, query_heads, kv_heads, head_dim, bits, key_codes,
                                 value_codes, key_scales, value_scales, capacity, seq_len, key_centroids,
                                 value_centroids, signs_left, signs_right, flags, current_keys, current_values,
-                                n_splits, workspace, out, stream, nullptr, nullptr);
+                                n_splits, workspace, workspace_bytes, out, stream, nullptr, nullptr);
 }
 
 int tq_decode_scaled_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
@@ -1933,61 +1944,62 @@ int tq_decode_scaled_timed(const void* query, int query_dtype, int num_layers, i
                            const float* key_scales, const float* value_scales, int64_t capacity, int64_t seq_len,
                            const float* key_centroids, const float* value_centroids, const float* signs_left,
                            const float* signs_right, int flags, const float* current_keys,
-                           const float* current_values, int n_splits, void* workspace, float* out,
-                           hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+                           const float* current_values, int n_splits, void* workspace, size_t workspace_bytes,
+                           float* out, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (!valid_bits(bits)) return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
   if (seq_len > 0 && (key_scales == nullptr || value_scales == nullptr))
     return fail(TQ_ERR_BAD_ARG, "key_scales and value_scales must be non-null");
   return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes, value_codes,
                        capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, flags,
-                       current_keys, current_values, n_splits, workspace, out, stream, start, stop, nullptr,
+                       current_keys, current_values, n_splits, workspace, workspace_bytes, out, stream, start, stop,
+                       nullptr,
                        seq_len > 0 ? key_scales : nullptr, seq_len > 0 ? value_scales : nullptr);
 }
 
-int tq_decode_append(const void* query, const void* new_keys, const void* new_values, int dtype, int num_layers,
-                     int query_heads, int kv_heads, int head_dim, int bits, uint32_t* key_codes,
+int tq_decode_append(const void* query, int query_dtype, const void* new_keys, const void* new_values, int kv_dtype,
+                     int num_layers, int query_heads, int kv_heads, int head_dim, int bits, uint32_t* key_codes,
                      uint32_t* value_codes, int64_t capacity, int64_t seq_len, const float* key_centroids,
                      const float* value_centroids, const float* key_boundaries, const float* value_boundaries,
                      const float* signs_left, const float* signs_right, int append_flags, int decode_flags,
-                     int n_splits, void* workspace, float* out, hipStream_t stream) {
+                     int n_splits, void* workspace, size_t workspace_bytes, float* out, hipStream_t stream) {
   int rc = check_geometry(head_dim, bits);
   if (rc) return rc;
-  const AppendSpec app{new_keys, new_values, key_boundaries, value_boundaries, append_flags};
-  return decode_common(bits, query, dtype, num_layers, query_heads, kv_heads, head_dim, key_codes, value_codes,
+  const AppendSpec app{new_keys, new_values, kv_dtype, key_boundaries, value_boundaries, append_flags};
+  return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes, value_codes,
                        capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, decode_flags,
-                       nullptr, nullptr, n_splits, workspace, out, stream, nullptr, nullptr, &app);
+                       nullptr, nullptr, n_splits, workspace, workspace_bytes, out, stream, nullptr, nullptr, &app);
 }
 
 int tq_decode_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
                     int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
                     int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,
                     const float* signs_left, const float* signs_right, int flags, const float* current_keys,
-                    const float* current_values, int n_splits, void* workspace, float* out, hipStream_t stream,
-                    hipEvent_t start, hipEvent_t stop) {
+                    const float* current_values, int n_splits, void* workspace, size_t workspace_bytes, float* out,
+                    hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (!valid_bits(bits)) return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
   return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes,
                        value_codes, capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, flags,
-                       current_keys, current_values, n_splits, workspace, out, stream, start, stop);
+                       current_keys, current_values, n_splits, workspace, workspace_bytes, out, stream, start, stop);
 }
 
 int tq_decode_dense(const void* query, int query_dtype, const void* keys, const void* values, int kv_dtype,
                     int num_layers, int query_heads, int kv_heads, int head_dim, int64_t capacity, int64_t seq_len,
                     const float* signs_left, const float* signs_right, int flags, int n_splits, void* workspace,
-                    float* out, hipStream_t stream) {
+                    size_t workspace_bytes, float* out, hipStream_t stream) {
   return tq_decode_dense_timed(query, query_dtype, keys, values, kv_dtype, num_layers, query_heads, kv_heads,
-                               head_dim, capacity, seq_len, signs_left, signs_right, flags, n_splits, workspace, out,
-                               stream, nullptr, nullptr);
+                               head_dim, capacity, seq_len, signs_left, signs_right, flags, n_splits, workspace,
+                               workspace_bytes, out, stream, nullptr, nullptr);
 }
 
 int tq_decode_dense_timed(const void* query, int query_dtype, const void* keys, const void* values, int kv_dtype,
                           int num_layers, int query_heads, int kv_heads, int head_dim, int64_t capacity,
                           int64_t seq_len, const float* signs_left, const float* signs_right, int flags,
-                          int n_splits, void* workspace, float* out, hipStream_t stream, hipEvent_t start,
-                          hipEvent_t stop) {
+                          int n_splits, void* workspace, size_t workspace_bytes, float* out, hipStream_t stream,
+                          hipEvent_t start, hipEvent_t stop) {
   if (kv_dtype != TQ_F16 && kv_dtype != TQ_F32) return fail(TQ_ERR_BAD_ARG, "kv dtype must be F32 or F16");
   return decode_common(kv_dtype == TQ_F16 ? 16 : 32, query, query_dtype, num_layers, query_heads, kv_heads, head_dim,
                        keys, values, capacity, seq_len, nullptr, nullptr, signs_left, signs_right, flags, nullptr,
-                       nullptr, n_splits, workspace, out, stream, start, stop);
+                       nullptr, n_splits, workspace, workspace_bytes, out, stream, start, stop);
 }
 
 int tq_score_packed(const float* query, const uint32_t* codes, int batch, int64_t seq_len, int head_dim, int bits,

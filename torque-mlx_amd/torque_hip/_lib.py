@@ -19,6 +19,8 @@ import torch  # noqa: F401  -- load torch's HIP runtime first
 LIB_NAME = "libtorque_hip.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
 
+ABI_VERSION = 2
+
 TQ_OK = 0
 TQ_ERR_BAD_ARG = -1
 TQ_ERR_UNSUPPORTED = -2
@@ -54,28 +56,30 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tq_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "tq_decode": (
         _i,
-        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _p],
+        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _sz, _p, _p],
     ),
     "tq_decode_scaled": (
         _i,
-        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _p],
+        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _sz, _p, _p],
     ),
     "tq_decode_scaled_timed": (
         _i,
-        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _p, _p, _p],
+        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _sz, _p, _p, _p,
+         _p],
     ),
     "tq_decode_timed": (
         _i,
-        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _p, _p, _p],
+        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _sz, _p, _p, _p, _p],
     ),
     "tq_decode_append": (
         _i,
-        [_p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p],
+        [_p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _sz, _p,
+         _p],
     ),
-    "tq_decode_dense": (_i, [_p, _i, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _p, _p, _i, _i, _p, _p, _p]),
+    "tq_decode_dense": (_i, [_p, _i, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _p, _p, _i, _i, _p, _sz, _p, _p]),
     "tq_decode_dense_timed": (
         _i,
-        [_p, _i, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _p, _p, _i, _i, _p, _p, _p, _p, _p],
+        [_p, _i, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _p, _p, _i, _i, _p, _sz, _p, _p, _p, _p],
     ),
     "tq_score_packed": (_i, [_p, _p, _i, _i64, _i, _i, _p, _p, _p]),
     "tq_softmax_rows": (_i, [_p, _i, _i64, _f, _p, _p]),
@@ -111,8 +115,8 @@ def load() -> ctypes.CDLL:
         fn.restype = restype
         fn.argtypes = argtypes
     version = lib.tq_abi_version()
-    if version != 1:
-        raise RuntimeError(f"libtorque_hip ABI version {version} does not match the bindings (1)")
+    if version != ABI_VERSION:
+        raise RuntimeError(f"libtorque_hip ABI version {version} does not match the bindings ({ABI_VERSION})")
     _LIB = lib
     return lib
 

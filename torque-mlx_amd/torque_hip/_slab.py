@@ -22,6 +22,18 @@ from torque_hip.quantization import Codebook, codebook_boundaries
 from torque_hip.rotation import RotationSpec
 
 
+def _kv_pair(keys: torch.Tensor, values: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """K/V in one dtype without rounding either: kept when they already agree, else both float32.
+
+    The reference quantizes float32 K/V (cache_mlx.py:442-466); float16 inputs
+    convert to float32 exactly in the kernels, so only a mixed pair needs a
+    cast, and it must go up, never down to the narrower type.
+    """
+    if keys.dtype != values.dtype:
+        keys, values = keys.to(torch.float32), values.to(torch.float32)
+    return keys.contiguous(), values.contiguous()
+
+
 class SlabStore:
     def __init__(
         self,
@@ -89,8 +101,7 @@ class SlabStore:
         seq_new = int(keys.shape[2])
         if seq_new == 0:
             return
-        if values.dtype != keys.dtype:
-            values = values.to(keys.dtype)
+        keys, values = _kv_pair(keys, values)
         self.ensure_capacity(self.length + seq_new)
         flags = (_lib.TQ_ROTATE_KEYS if rotate_keys else 0) | (_lib.TQ_ROTATE_VALUES if rotate_values else 0)
         cfg = self.config
@@ -124,8 +135,7 @@ class SlabStore:
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """Rotate -> quantize -> dequantize one token per (layer, KV head): [L, Hkv, 1, D] -> [L, Hkv, D]."""
         cfg = self.config
-        if values.dtype != keys.dtype:
-            values = values.to(keys.dtype)
+        keys, values = _kv_pair(keys, values)
         rows = cfg.num_layers * cfg.kv_heads
         k_out = torch.empty((cfg.num_layers, cfg.kv_heads, cfg.head_dim), dtype=torch.float32, device=self.device)
         v_out = torch.empty_like(k_out)
@@ -211,9 +221,7 @@ class SlabStore:
             return out
         cfg = self.config
         self.ensure_capacity(self.length + 1)
-        dtype = queries.dtype
-        keys = keys.to(dtype).contiguous()
-        values = values.to(dtype).contiguous()
+        keys, values = _kv_pair(keys, values)
         out = packed_decode_append(
             queries,
             keys,

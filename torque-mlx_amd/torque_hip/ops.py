@@ -44,10 +44,11 @@ def _as_uint32(t: torch.Tensor) -> torch.Tensor:
 
 
 class Workspace:
-    """Zero-initialised split-K workspace, one per (device, stream), grown on demand.
+    """Split-K workspace, one per (device, stream), grown on demand.
 
-    The decode kernels leave its counters at zero when they finish, so calls
-    ordered on one stream can share it.
+    It holds the per-split partial results between the split kernel and the
+    merge kernel of one decode call; every call overwrites what it reads, so
+    calls ordered on one stream can share it.
     """
 
     _pool: dict[tuple[str, int], torch.Tensor] = {}
@@ -141,6 +142,7 @@ def packed_decode(
         None if current_values is None else current_values.data_ptr(),
         n_splits,
         ws.data_ptr(),
+        ws.numel(),
         out.data_ptr(),
         stream_handle(dev),
     )
@@ -175,7 +177,10 @@ def packed_decode_append(
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One ``tq_decode_append`` launch: pack the new token [L, Hkv, D] into the slabs at row ``seq_len`` and
-    decode over the ``seq_len + 1`` tokens; query, new_keys and new_values share one dtype."""
+    decode over the ``seq_len + 1`` tokens.  new_keys and new_values share one dtype (float32 or float16), which
+    need not be the query's: the token is quantized from its own values."""
+    if new_keys.dtype != new_values.dtype:
+        raise ValueError("new_keys and new_values must share one dtype")
     dev = query.device
     if n_splits is None or n_splits <= 0:
         n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev)
@@ -187,9 +192,10 @@ def packed_decode_append(
     _lib.call(
         "tq_decode_append",
         query.data_ptr(),
+        dtype_code(query),
         new_keys.data_ptr(),
         new_values.data_ptr(),
-        dtype_code(query),
+        dtype_code(new_keys),
         num_layers,
         query_heads,
         kv_heads,
@@ -209,6 +215,7 @@ def packed_decode_append(
         decode_flags,
         n_splits,
         ws.data_ptr(),
+        ws.numel(),
         out.data_ptr(),
         stream_handle(dev),
     )
@@ -259,6 +266,7 @@ def dense_decode(
         flags,
         n_splits,
         ws.data_ptr(),
+        ws.numel(),
         out.data_ptr(),
         stream_handle(dev),
     )

@@ -222,13 +222,13 @@ class QwenDecodeRuntimeBenchmarkResult:
     fp16_update_seconds: float
     fp16_attention_seconds: float
     fp16_decode_seconds: float
-    mlx_lm_quantized_update_seconds: float
-    mlx_lm_quantized_attention_seconds: float
-    mlx_lm_quantized_decode_seconds: float
+    mlx_lm_quantized_update_seconds: float | None
+    mlx_lm_quantized_attention_seconds: float | None
+    mlx_lm_quantized_decode_seconds: float | None
     torque_append_seconds: float
     torque_kernel_seconds: float
     torque_decode_seconds: float
-    max_abs_error_quantized_vs_fp16: float
+    max_abs_error_quantized_vs_fp16: float | None
     max_abs_error_torque_vs_fp16: float
 
     def to_dict(self) -> dict[str, object]:
@@ -243,6 +243,12 @@ class QwenDecodeRuntimeBenchmarkResult:
 
         def tps(seconds: float) -> float:
             return self.decode_steps / seconds if seconds > 0 else 0.0
+
+        def ms(seconds: float | None) -> float | None:
+            return None if seconds is None else seconds * 1_000.0
+
+        # MLX-LM's quantized comparator does not exist on this backend: its figures are reported as null.
+        quantized_absent = self.mlx_lm_quantized_decode_seconds is None
 
         fp16 = {
             "update_ms": self.fp16_update_seconds * 1_000.0,
@@ -264,22 +270,23 @@ class QwenDecodeRuntimeBenchmarkResult:
                 "This benchmark measures the KV-growing decode hot path only, not full dense forwards or perplexity.",
                 "It uses the Qwen model geometry from the local snapshot or torque manifest.",
                 "Backend: HIP on MI355X. mlx_fp16_* report the fp16-dense HIP decode kernel; "
-                "MLX-LM's QuantizedKVCache has no counterpart (mlx_lm_quantized_* are zero).",
+                "MLX-LM's QuantizedKVCache has no counterpart: mlx_lm_quantized_* and "
+                "max_abs_error_quantized_vs_fp16 are null.",
             ],
             "fp16_kv_cache_total_bytes": fp16_total,
             "torque_kv_cache_total_bytes": torque_total,
             "fp16_kv_cache_total_gib": fp16_total / float(1 << 30),
             "torque_kv_cache_total_gib": torque_total / float(1 << 30),
             "kv_cache_bytes_saved_vs_fp16": fp16_total - torque_total,
-            "mlx_lm_quantized_update_ms": self.mlx_lm_quantized_update_seconds * 1_000.0,
-            "mlx_lm_quantized_attention_ms": self.mlx_lm_quantized_attention_seconds * 1_000.0,
-            "mlx_lm_quantized_host_overhead_ms": host(
+            "mlx_lm_quantized_update_ms": ms(self.mlx_lm_quantized_update_seconds),
+            "mlx_lm_quantized_attention_ms": ms(self.mlx_lm_quantized_attention_seconds),
+            "mlx_lm_quantized_host_overhead_ms": None if quantized_absent else host(
                 self.mlx_lm_quantized_decode_seconds,
                 self.mlx_lm_quantized_update_seconds,
                 self.mlx_lm_quantized_attention_seconds,
             ) * 1_000.0,
-            "mlx_lm_quantized_decode_ms": self.mlx_lm_quantized_decode_seconds * 1_000.0,
-            "mlx_lm_quantized_tokens_per_sec": tps(self.mlx_lm_quantized_decode_seconds),
+            "mlx_lm_quantized_decode_ms": ms(self.mlx_lm_quantized_decode_seconds),
+            "mlx_lm_quantized_tokens_per_sec": None if quantized_absent else tps(self.mlx_lm_quantized_decode_seconds),
             "torque_mlx_append_ms": self.torque_append_seconds * 1_000.0,
             "torque_mlx_kernel_ms": self.torque_kernel_seconds * 1_000.0,
             "torque_mlx_host_overhead_ms": host(
@@ -460,13 +467,13 @@ def _run_qwen_decode_runtime_benchmark_impl(
         fp16_update_seconds=fp16_update,
         fp16_attention_seconds=fp16_attention,
         fp16_decode_seconds=fp16_elapsed,
-        mlx_lm_quantized_update_seconds=0.0,
-        mlx_lm_quantized_attention_seconds=0.0,
-        mlx_lm_quantized_decode_seconds=0.0,
+        mlx_lm_quantized_update_seconds=None,
+        mlx_lm_quantized_attention_seconds=None,
+        mlx_lm_quantized_decode_seconds=None,
         torque_append_seconds=append_elapsed,
         torque_kernel_seconds=kernel_elapsed,
         torque_decode_seconds=torque_elapsed,
-        max_abs_error_quantized_vs_fp16=0.0,
+        max_abs_error_quantized_vs_fp16=None,
         max_abs_error_torque_vs_fp16=float(np.max(np.abs(torque_final - fp16_final))),
     )
 
