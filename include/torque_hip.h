@@ -149,6 +149,24 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
               const float* current_values, int n_splits, void* workspace, size_t workspace_bytes, float* out,
               hipStream_t stream);
 
+/* tq_decode without a caller workspace and without allocating: the split-K
+ * partials go to a static scratch array of 8 MiB held by the library on each
+ * GPU (device memory, kept until the process ends; its address is looked up
+ * once per device on the first call there).  No counterpart in the reference:
+ * it is for callers that cannot allocate -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc -- and calls no
+ * hipMalloc, hipFree or other allocating routine.  Same arguments and results
+ * as tq_decode minus the workspace.  A call whose resolved split plan needs
+ * more than 8 MiB (tq_decode_workspace_bytes) returns TQ_ERR_BAD_ARG before
+ * any launch; pass fewer splits or fewer layers.  Every call on one GPU shares
+ * that GPU's scratch: calls that overlap on one GPU (different streams, or
+ * threads without ordering) race and must not be issued. */
+int tq_decode_noalloc(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
+                      int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
+                      int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,
+                      const float* signs_left, const float* signs_right, int flags, const float* current_keys,
+                      const float* current_values, int n_splits, float* out, hipStream_t stream);
+
 /* tq_decode over slabs written by tq_append_scaled: a token's score is
  * multiplied by its key scale and its value by its value scale (scales
  * [L, Hkv, capacity] float32).  current_keys / current_values, when given,

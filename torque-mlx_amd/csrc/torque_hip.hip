@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -1230,6 +1231,47 @@ WsLayout workspace_layout(int64_t lq, int64_t lkv, int head_dim, int n_splits) {
   return w;
 }
 
+// ---- static scratch of the no-allocation decode entry point.
+// One array per GPU in device memory, held until the process ends; every
+// tq_decode_noalloc call on a GPU uses that GPU's copy as its split-K
+// workspace (which needs no initialisation: each call writes every partial it
+// later reads), so calls that overlap on one GPU race.  In host code
+// `scratch` only names the symbol: its device address comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address (looked up on the first call on that
+// device), or nullptr with the error set.
+void* device_scratch() {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(TQ_ERR_LAUNCH, std::string("tq_decode_noalloc: no current HIP device: ") + hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(TQ_ERR_UNSUPPORTED, "tq_decode_noalloc: device index " + std::to_string(dev) + " out of range");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (r != hipSuccess || ptr == nullptr) {
+      fail(TQ_ERR_LAUNCH, std::string("tq_decode_noalloc: hipGetSymbolAddress(scratch) failed: ") +
+                              hipGetErrorString(r));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
 // Fills the split plan.  block_rows: rows per workgroup iteration of the
 // kernel that will run (the unit the sequence is dealt out in); every split
 // gets at least one block.
@@ -1254,6 +1296,16 @@ int make_plan(int num_layers, int kv_heads, int query_heads, int64_t seq_len, in
   const int64_t blocks = std::max<int64_t>(1, (seq_len + block_rows - 1) / block_rows);
   p->n_splits = static_cast<int>(std::min<int64_t>({blocks, static_cast<int64_t>(ns), max_wg / units}));
   return TQ_OK;
+}
+
+// Rows per workgroup iteration of the decode kernel for `fmt` (2/3/4 packed
+// bits, 16 dense fp16, 32 dense fp32): tokens per lane group x lane groups
+// per wavefront (64 / (D / slice dims)) x wavefronts; packed slices hold 16
+// dimensions, fp16 rows 8, fp32 rows 4.
+int decode_block_rows(int fmt, int head_dim) {
+  const bool packed = fmt == 2 || fmt == 3 || fmt == 4;
+  const int slice_dims = packed ? 16 : (fmt == 16 ? 8 : 4);
+  return kTokensPerIter * kWavesPerBlock * kWave * slice_dims / head_dim;
 }
 
 template <class Fmt, int D, int HG, bool QF16, bool SC>
@@ -1367,12 +1419,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   if (capacity * row_bytes >= (1LL << 31))
     return fail(TQ_ERR_BAD_ARG, "capacity * row bytes must stay below 2 GiB per (layer, KV head)");
   Plan p;
-  // Rows per workgroup iteration: tokens per lane group x lane groups per
-  // wavefront (64 / (D / slice dims)) x wavefronts; packed slices hold 16
-  // dimensions, fp16 rows 8, fp32 rows 4.
-  const int slice_dims = packed ? 16 : (fmt == 16 ? 8 : 4);
-  const int block_rows = kTokensPerIter * kWavesPerBlock * kWave * slice_dims / head_dim;
-  rc = make_plan(num_layers, kv_heads, query_heads, seq_len, n_splits, block_rows, &p);
+  rc = make_plan(num_layers, kv_heads, query_heads, seq_len, n_splits, decode_block_rows(fmt, head_dim), &p);
   if (rc) return rc;
   if (p.n_splits > 1 &&
       static_cast<int64_t>(num_layers) * query_heads * (head_dim / kMergeDims) > ((int64_t(1) << 32) - 1) / kBlock)
@@ -1925,6 +1972,34 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
                          value_codes, capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right,
                          flags, current_keys, current_values, n_splits, workspace, workspace_bytes, out, stream,
                          nullptr, nullptr);
+}
+
+int tq_decode_noalloc(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
+                      int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
+                      int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,
+                      const float* signs_left, const float* signs_right, int flags, const float* current_keys,
+                      const float* current_values, int n_splits, float* out, hipStream_t stream) {
+  if (!valid_bits(bits)) return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
+  int rc = check_geometry(head_dim, bits);
+  if (rc) return rc;
+  // The split plan this call resolves to, and the scratch it needs, before
+  // anything touches the device.
+  Plan p;
+  rc = make_plan(num_layers, kv_heads, query_heads, seq_len, n_splits, decode_block_rows(bits, head_dim), &p);
+  if (rc) return rc;
+  const size_t need = workspace_layout(static_cast<int64_t>(num_layers) * query_heads,
+                                       static_cast<int64_t>(num_layers) * kv_heads, head_dim, p.n_splits)
+                          .total;
+  if (need > kScratchBytes)
+    return fail(TQ_ERR_BAD_ARG, "tq_decode_noalloc: this call needs " + std::to_string(need) +
+                                    " bytes of scratch (" + std::to_string(p.n_splits) +
+                                    " splits) but the static scratch holds " + std::to_string(kScratchBytes) +
+                                    "; pass fewer splits or decode fewer layers per call");
+  void* ws = device_scratch();
+  if (ws == nullptr) return TQ_ERR_LAUNCH;
+  return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes,
+                       value_codes, capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, flags,
+                       current_keys, current_values, p.n_splits, ws, kScratchBytes, out, stream, nullptr, nullptr);
 }
 
 int tq_decode_scaled(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads, int head_dim,

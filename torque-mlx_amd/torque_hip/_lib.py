@@ -58,6 +58,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i,
         [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _sz, _p, _p],
     ),
+    "tq_decode_noalloc": (
+        _i,
+        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _p],
+    ),
     "tq_decode_scaled": (
         _i,
         [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _sz, _p, _p],
