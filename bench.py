@@ -223,7 +223,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
 
     stores = [c._store for c in caches]
     w = stores[0].layout.packed_words
-    n_splits = [ops.plan_splits(1, hkv, hq, d, s0 + steps, dev) for _ in range(L)]
+    n_splits = [ops.plan_splits(1, hkv, hq, d, s0 + steps, dev, bit_width=bits) for _ in range(L)]
     ws = ops.workspace_for(1, hkv, hq, d, args.splits, dev)
     out = torch.empty((L, hq, d), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
@@ -483,7 +483,7 @@ def main() -> int:
         torch.randn((L, hq, d), generator=torch.Generator(device=dev).manual_seed(i), device=dev).half()
         for i in range(1, 4)
     ]
-    n_splits = args.splits or ops.plan_splits(L, hkv, hq, d, s, dev)
+    n_splits = args.splits or ops.plan_splits(L, hkv, hq, d, s, dev, bit_width=bits)
     ws = ops.workspace_for(L, hkv, hq, d, n_splits, dev)
     out = torch.empty((L, hq, d), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream

@@ -41,8 +41,12 @@ enum { TQ_F32 = 0, TQ_F16 = 1 };
 
 /* tq_append / tq_quantize_dequantize flags (reference cache_mlx.py:52-54) */
 enum { TQ_ROTATE_KEYS = 1, TQ_ROTATE_VALUES = 2 };
-/* tq_decode / tq_decode_dense flags (reference cache_mlx.py:188-196, 225-232) */
-enum { TQ_ROTATE_QUERY = 1, TQ_INVERSE_OUTPUT = 2 };
+/* tq_decode / tq_decode_dense flags (reference cache_mlx.py:188-196, 225-232).
+ * TQ_F32_PRODUCTS (no reference counterpart) selects the float32 split kernel
+ * where the float16-split matrix kernel would run (4-bit rows, groups of 4
+ * query heads, head_dim 64 / 128); both accumulate in float32.  tq_decode_scaled
+ * always runs the float32 split kernel. */
+enum { TQ_ROTATE_QUERY = 1, TQ_INVERSE_OUTPUT = 2, TQ_F32_PRODUCTS = 4 };
 
 int tq_abi_version(void);
 const char* tq_last_error(void);
@@ -114,12 +118,13 @@ int tq_unpack_dequantize_scaled(const uint32_t* codes, const float* scales, int6
                                 int64_t seq_len, int head_dim, int bits, const float* centroids, float* out,
                                 hipStream_t stream);
 
-/* Split count the decode kernels use when n_splits <= 0 is passed.  The
- * sequence is dealt out to the splits in blocks of one workgroup iteration
- * (split s takes blocks s, s + n, s + 2n, ...); an explicit n_splits above
- * the number of blocks is lowered to it. */
-int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int head_dim, int64_t seq_len,
-                             int num_cus);
+/* Split count a decode call over `bits`-bit rows (0 for dense rows) with
+ * decode `flags` uses when n_splits <= 0 is passed.  The sequence is dealt
+ * out to the splits in blocks of one workgroup iteration (split s takes
+ * blocks s, s + n, s + 2n, ...); an explicit n_splits above the number of
+ * blocks is lowered to it. */
+int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int head_dim, int bits, int flags,
+                             int64_t seq_len, int num_cus);
 
 /* Bytes of workspace tq_decode / tq_decode_dense need for n_splits splits
  * (n_splits <= 0: enough for the default split count on any sequence length

@@ -46,8 +46,12 @@ def test_host_only_entry_points():
 
     lib = _lib.load()
     assert lib.tq_abi_version() == _lib.ABI_VERSION == 2
-    assert lib.tq_decode_default_splits(1, 8, 32, 128, 32768, 256) == 64
-    assert lib.tq_decode_default_splits(1, 8, 32, 128, 7, 256) == 1
+    # 4-bit rows in groups of 4 query heads: the f16-split matrix kernel, one 512-thread workgroup per CU
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 32768, 256) == 32
+    # the float32-product kernel (requested, or 2-bit rows): two 256-thread workgroups per CU
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 4, 32768, 256) == 64
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 2, 0, 32768, 256) == 64
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 7, 256) == 1
     assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, 64, 256) > 64 * 8 * 4 * 128 * 4
     assert lib.tq_decode_workspace_bytes(1, 8, 30, 128, 64, 256) == 0  # Hq not divisible
 
@@ -128,7 +132,7 @@ def test_workspace_query_covers_default_plan():
 
     lib = _lib.load()
     for seq_len in (1, 100, 4096, 32768, 1 << 20):
-        ns = lib.tq_decode_default_splits(1, 8, 32, 128, seq_len, 256)
+        ns = max(lib.tq_decode_default_splits(1, 8, 32, 128, bits, 0, seq_len, 256) for bits in (0, 2, 3, 4))
         assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, ns, 256) <= lib.tq_decode_workspace_bytes(1, 8, 32, 128, 0,
                                                                                                         256)
 

@@ -124,7 +124,7 @@ def test_c3_and_metric_shape_32k(hip_device, bits):
     for ns in (8, 17, 256):
         other = store.decode(q, rotate_query=True, inverse_output=True, n_splits=ns).cpu().numpy()
         np.testing.assert_allclose(other, out, atol=1e-6, rtol=1e-5, err_msg=f"n_splits {ns}")
-    assert ops.plan_splits(1, 8, 32, 128, 32768, hip_device) > 1
+    assert ops.plan_splits(1, 8, 32, 128, 32768, hip_device, bit_width=4) > 1
 
 
 def test_c4_qwen_style_128k(hip_device):

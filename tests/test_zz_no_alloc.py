@@ -2,8 +2,11 @@
 
 Its split-K partials live in the library's static per-GPU scratch array.  Two
 calls in a row -- the second smaller than the first, so it runs over what the
-first left in the scratch -- each give exactly tq_decode's output on the same
-inputs (same kernels, same split plan).
+first left in the scratch -- each give tq_decode's output on the same inputs:
+the same kernels and split plan, so the outputs agree to float32 rounding (the
+split kernel's wavefronts claim tiles dynamically, so the order in which a
+workgroup adds its tiles, and with it the last bits, can differ between any two
+calls).
 """
 
 from __future__ import annotations
@@ -41,7 +44,8 @@ def _both(dev, cache, query, n_splits):
               st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, st.length, st.key_centroids.data_ptr(),
               st.value_centroids.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), flags, None, None,
               n_splits)
-    ns = n_splits if n_splits > 0 else ops.plan_splits(1, cfg.kv_heads, hq, cfg.head_dim, st.length, dev)
+    ns = n_splits if n_splits > 0 else ops.plan_splits(1, cfg.kv_heads, hq, cfg.head_dim, st.length, dev,
+                                                       bit_width=cfg.bit_width)
     ws = torch.empty(_lib.call("tq_decode_workspace_bytes", 1, cfg.kv_heads, hq, cfg.head_dim, ns, ops.num_cus(dev)),
                      dtype=torch.uint8, device=dev)
     ref = torch.empty((1, hq, cfg.head_dim), dtype=torch.float32, device=dev)
@@ -61,7 +65,7 @@ def test_noalloc_matches_decode_on_two_calls(hip_device):
     for cache, q, ns in ((big, q_big, 0), (small, q_small, 0), (small, q_small, 3), (big, q_big, 1)):
         ref, got = _both(hip_device, cache, q, ns)
         assert np.isfinite(ref).all()
-        np.testing.assert_array_equal(got, ref)
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
 
 
 def test_noalloc_rejects_oversized_plan(hip_device):

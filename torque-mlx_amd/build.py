@@ -3,7 +3,10 @@
     python torque-mlx_amd/build.py            # or __graft_entry__.build()
 
 Compiles csrc/torque_hip.hip with hipcc into torque_hip/libtorque_hip.so,
-in-tree.  Packed-FP32 VALU ops are disabled for all device code.
+in-tree.  Packed-FP32 VALU ops are disabled for all device code.  The
+atomic optimizer is off for device code: it rewrites a single lane's LDS
+atomic (the split kernels' tile counter) into a wave-wide form that waits
+for the result at once, where the kernels want it one iteration later.
 """
 
 from __future__ import annotations
@@ -30,6 +33,8 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-Xarch_device",
+    "-mllvm=-amdgpu-atomic-optimizer-strategy=None",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -1,0 +1,624 @@
+// decode_mx_kernel -- split-K packed decode for groups of 4 query heads on the
+// gfx950 matrix cores with 16x16x32 float16 products (v_mfma_f32_16x16x32_f16).
+//
+// Included by torque_hip.hip (uses DecodeArgs, finish_row and tq_device.hpp).
+//
+// Arithmetic.  Every product is formed from exact float16 splits and summed in
+// float32: a centroid c is stored as hi = f16(c) and lo = f16(c - hi) (so
+// |c - hi - lo| <= 2^-22 |c|), the scaled query q likewise, and a softmax
+// weight p as hi = p with its low 13 mantissa bits cleared (exact in f16) and
+// lo = f16(p - hi).  The products hi*hi, hi*lo, lo*hi, lo*lo are exact in
+// float32, so a score or value term carries at most ~2^-21 relative error
+// against the float32 product (2^-24), and every sum is a float32 sum.
+// Before splitting, the centroids, the query and the weights are scaled by
+// powers of two (exact) so that their largest magnitude sits in
+// [2^14, 2^15): no f16 overflow, and the lo parts stay clear of f16
+// subnormals for all but negligible terms.  The scales are undone with one
+// exact multiply per score and per output.  Per-vector scales (the scaled
+// decode) are not taken here: they would multiply the weights, whose split
+// has no headroom for a factor of unknown size; that decode runs on the
+// float32 split kernel.
+//
+// Lane layouts (wave of 64 lanes; n = lane % 16, g = lane / 16; checked on the
+// device: the A operand of lane l supplies row l % 16, the B operand column
+// l % 16, both with the 8 k-slots of lane group g, and the 16x16 result holds
+// column l % 16, rows 4g .. 4g + 3 in its 4 registers).
+//
+//   A wave takes 16 consecutive rows (tokens) per iteration: token 4g + r is
+//   row r of lane group g's part of every result tile.
+//
+//   Scores, S[token][col] += K[token][k] * Q[k][col]: A = key rows, lane
+//   (n, g) holding token n and the g-th quarter of its packed row (a 128-bit
+//   load at D = 128); each key byte (two codes, dims 2i, 2i + 1) is one lookup
+//   in a table of (hi pair, lo pair) and fills k-slots (hi(d), hi(d+1),
+//   lo(d), lo(d+1)), so one 16x16x32 product covers 4 dims per lane group.
+//   B = the query: column h holds the hi split of head h's query, column
+//   4 + h its lo split, columns 8..15 zero; each query value appears in the
+//   k-slots of both the hi and the lo key part.  The score of head h is
+//   column h + column 4 + h (a row_ror:12 DPP add: lane i reads lane i + 4 of
+//   its row), so lanes n < 4 end up with
+//   head n's scores of their 4 tokens.
+//
+//   Values, O[row][dim] += P[row][k] * V[k][dim]: B = value codes, lane
+//   (n, g) reading dword n (8 dims) of rows 4g .. 4g + 3; the nibbles of a
+//   dim in two tokens are interleaved into one byte, whose lookup in the
+//   value table gives (hi(t), hi(t')) and (lo(t), lo(t')), so the k-slots are
+//   4 tokens x (hi, lo).  A = weights: row h holds the hi split of head h's
+//   weights, row 4 + h the lo split (moved there from lanes 0..3 by a
+//   row_shr:4 DPP move), in the k-slots of both the hi and lo value part.
+//   One product covers 16 tokens x 16 dims; the output of head h is row h +
+//   row 4 + h (lane groups 0 and 1, one permlane16 swap at the end).
+//
+// Tables: 256 entries x 8 bytes per stream, each entry replicated 32 times
+// so that lane l reads copy l % 32: entry e, copy c at byte e * 256 + c * 8
+// (64 KB per stream), which keeps 32 lanes' 8-byte reads on 32 distinct bank
+// pairs whatever the codes (measured: 2.96 cycles per wave read against 6.6
+// for one shared 2 KB table).  The key table sits at LDS byte 0, the value
+// table at 65536, so a lookup address is one v_perm_b32 that puts the code
+// byte in bits 8..15 of the lane's base.
+
+namespace mx {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 12;                // wavefronts per workgroup (3 per SIMD)
+constexpr int kThreads = kWaves * kWave;  // 768: one workgroup per compute unit
+constexpr int kTile = 16;                 // tokens per wavefront iteration
+constexpr int kTilesPerBlock = 8;
+constexpr int kStride = kTilesPerBlock * kTile;  // rows per block (the unit dealt out to the splits)
+constexpr int kCopies = 32;               // lane-private copies of a table entry
+constexpr int kTableBytes = 256 * kCopies * 8;
+constexpr int kPrefetch = 2;              // tiles whose loads are in flight ahead
+
+// LDS: the two tables, reused for the cross-wavefront reduction after the loop.
+template <int D>
+struct Smem {
+  static constexpr int kQbStride = D + 8;                // f16 elements per padded row (16-byte skew per row)
+  static constexpr int kQbBytes = 8 * kQbStride * 2;     // f16 query splits [8 cols][D]
+  static constexpr int kQBytes = 4 * D * 4;           // float32 scaled query [4][D]
+  static constexpr int kCurBytes = 2 * D * 4 + 2 * D;  // append mode: s_cur [2][D] + codes [2][D]
+  static constexpr int kMisc = 1024;
+  static constexpr int kStageBytes = 2 * 256 * 8;       // one copy of each table, staged before replication
+  static constexpr int kRedBytes = kWaves * 4 * D * 4;  // after the loop, inside the table area
+  static constexpr int kQb = 2 * kTableBytes;
+  static constexpr int kQ = kQb + kQbBytes;
+  static constexpr int kCur = kQ + kQBytes;
+  static constexpr int kMiscOff = kCur + kCurBytes;
+  static constexpr int kStage = kMiscOff + kMisc;
+  static constexpr int kTotal = kStage + kStageBytes;
+  static_assert(kRedBytes + 2 * kWaves * 4 * 4 <= 2 * kTableBytes, "reduction fits in the table area");
+};
+
+__device__ __forceinline__ uint32_t pack_f16x2(_Float16 lo, _Float16 hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+}
+
+// Largest magnitude of x[0..n) -> exponent shift that maps it into [2^14, 2^15).
+__device__ __forceinline__ int scale_shift(float maxabs) {
+  if (!(maxabs > 0.f) || !isfinite(maxabs)) return 0;
+  int e;
+  frexpf(maxabs, &e);  // maxabs = m 2^e, m in [0.5, 1)
+  return 15 - e;
+}
+
+// Byte k of w placed in bits 8..15 of the lane's table base (bits 0..7 and
+// 16..31 of `base`): the lookup address of code byte k.
+template <int K>
+__device__ __forceinline__ uint32_t lut_addr(uint32_t w, uint32_t base) {
+  return __builtin_amdgcn_perm(w, base, 0x03020000u | ((4u + K) << 8));
+}
+__device__ __forceinline__ uint32_t lut_addr_dyn(uint32_t w, uint32_t base, int k) {
+  switch (k & 3) {
+    case 0:
+      return lut_addr<0>(w, base);
+    case 1:
+      return lut_addr<1>(w, base);
+    case 2:
+      return lut_addr<2>(w, base);
+    default:
+      return lut_addr<3>(w, base);
+  }
+}
+
+__device__ __forceinline__ uint2 lds_read_u2(const uint8_t* smem, uint32_t addr) {
+  return *reinterpret_cast<const uint2*>(smem + addr);
+}
+
+__device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(f16x8, u32x4{a, b, c, d});
+}
+
+__device__ __forceinline__ int table_shift(const float* __restrict__ cent) {
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(cent[j]));
+  return scale_shift(mx);
+}
+
+// Table entry e of one stream from its two centroids ce0 = c[e & 15],
+// ce1 = c[e >> 4]: (hi(ce0), hi(ce1)), (lo(ce0), lo(ce1)) of the centroids
+// scaled by 2^sh.
+__device__ __forceinline__ uint2 table_entry(float ce0, float ce1, int sh) {
+  const float c0 = ldexpf(ce0, sh), c1 = ldexpf(ce1, sh);
+  const _Float16 h0 = static_cast<_Float16>(c0), h1 = static_cast<_Float16>(c1);
+  const _Float16 l0 = static_cast<_Float16>(c0 - static_cast<float>(h0));
+  const _Float16 l1 = static_cast<_Float16>(c1 - static_cast<float>(h1));
+  return make_uint2(pack_f16x2(h0, h1), pack_f16x2(l0, l1));
+}
+
+// Replicates the staged entries (stage[t][e], t = 0 keys, 1 values) into the
+// two 64 KB tables, in 128 spans of 1 KB: wavefront w writes spans w,
+// w + kWaves, ..., lane l the 16 bytes (two copies) at 1 KB * span + 16 l.
+// Each write instruction covers 1 KB contiguously (no bank conflicts) and its
+// lanes read 4 distinct staged entries (broadcast reads).
+__device__ __forceinline__ void replicate_tables(uint8_t* smem, const uint2* stage, int wave, int lane) {
+  constexpr int kSpans = 2 * kTableBytes / 1024;
+  constexpr int kSteps = (kSpans + kWaves - 1) / kWaves;
+  // All reads before all writes: the compiler cannot tell the staged entries
+  // from the tables (one shared array), so interleaving would serialize
+  // every read behind the previous write.
+  uint2 v[kSteps];
+#pragma unroll
+  for (int k = 0; k < kSteps; ++k) {
+    const int span = min(wave + k * kWaves, kSpans - 1);  // a wavefront past the end rewrites the last span
+    const int off = (span << 10) + (lane << 4);
+    v[k] = stage[((off >> 16) << 8) + ((off >> 8) & 255)];
+  }
+#pragma unroll
+  for (int k = 0; k < kSteps; ++k) {
+    const int span = min(wave + k * kWaves, kSpans - 1);
+    const int off = (span << 10) + (lane << 4);
+    *reinterpret_cast<uint4*>(smem + off) = make_uint4(v[k].x, v[k].y, v[k].x, v[k].y);
+  }
+}
+
+}  // namespace mx
+
+template <int D, bool QF16>
+__global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_mx_kernel(
+    const DecodeArgs a) {
+  using namespace mx;
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128 or 256");
+  constexpr int ROW = D / 2;          // packed bytes per row (4-bit)
+  constexpr int KB = ROW / 4;         // key bytes per lane per tile (a quarter row)
+  constexpr int KW = (KB + 3) / 4;    // key dwords per lane (KB = 8, 16, 32)
+  constexpr int NS = D / 16;          // score products per tile
+  constexpr int NV = D / 16;          // value products per tile
+  constexpr int VW = D == 256 ? 2 : 1;  // value dwords per lane per row
+  constexpr int E = D / kWave;
+  using L = Smem<D>;
+
+  __shared__ __align__(16) uint8_t smem[L::kTotal];
+  uint16_t* s_qb = reinterpret_cast<uint16_t*>(smem + L::kQb);  // [8][D] f16 bits
+  float* s_q = reinterpret_cast<float*>(smem + L::kQ);           // [4][D]
+  float* s_cur = reinterpret_cast<float*>(smem + L::kCur);       // [2][D]
+  uint8_t* s_codes = smem + L::kCur + 2 * D * 4;                 // [2][D]
+  float* s_misc = reinterpret_cast<float*>(smem + L::kMiscOff);  // [0..3] score scale per head, [4..7] shifts
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: row ranges and resources stay scalar
+  const int n = lane & 15, g = lane >> 4;
+
+  // ---- work item (same XCD remap as decode_kernel: the splits of one head
+  // group share one XCD's L2).
+  const int units = a.num_layers * a.kv_heads * a.n_hgroups;
+  const int64_t nblk = static_cast<int64_t>(units) * a.n_splits;
+  int64_t gid = blockIdx.x;
+  if ((nblk & 7) == 0) gid = (gid & 7) * (nblk >> 3) + (gid >> 3);
+  const int unit = static_cast<int>(gid / a.n_splits);
+  const int split = static_cast<int>(gid - static_cast<int64_t>(unit) * a.n_splits);
+  const int lkv = unit / a.n_hgroups;
+  const int hg = unit - lkv * a.n_hgroups;
+  const int layer = lkv / a.kv_heads, kvh = lkv - layer * a.kv_heads;
+  const int qh0 = kvh * a.group + hg * 4;
+
+  // Rows: blocks of kStride rows dealt out cyclically over the splits (split
+  // s takes blocks s, s + n, s + 2n, ...), each block cut into
+  // kTilesPerBlock tiles of 16 rows.  Tile k of this split is tile
+  // k % kTilesPerBlock of its (k / kTilesPerBlock)-th block.  Wavefronts
+  // claim tiles: the first kPrefetch rounds statically (tile j * kWaves +
+  // wave), then from a counter in LDS, so a wavefront that runs ahead takes
+  // more tiles and all finish within about a tile of each other.  Row offsets
+  // are 32-bit (the host keeps capacity * ROW < 2^31).
+  const int t1 = static_cast<int>(a.seq_len);
+  const int BSTRIDE = a.n_splits * kStride;
+  const int n_blocks = (t1 + kStride - 1) / kStride;
+  const int n_iter = split < n_blocks ? (n_blocks - split + a.n_splits - 1) / a.n_splits : 0;
+  const int n_tiles = n_iter * kTilesPerBlock;
+  auto tile_row = [&](int k) {
+    const unsigned uk = static_cast<unsigned>(k);
+    return split * kStride + static_cast<int>(uk / kTilesPerBlock) * BSTRIDE + static_cast<int>(uk % kTilesPerBlock) * kTile;
+  };
+  const uint8_t* kbase = a.k + static_cast<int64_t>(lkv) * a.cap * ROW;
+  const uint8_t* vbase = a.v + static_cast<int64_t>(lkv) * a.cap * ROW;
+
+  // Per-lane load offsets inside a tile: key quarter g of row n; value dword
+  // n (and 16 + n at D = 256; dword n / 2 at D = 64) of rows 4g + r.
+  const int koff = n * ROW + g * KB;
+  const int voff = (4 * g) * ROW + 4 * (D == 64 ? (n >> 1) : n);
+  struct Raw {
+    uint32_t k[KW];
+    uint32_t v[4][VW];
+  };
+  auto load_tile = [&](int k, Raw& r) {
+    const int row0 = min(tile_row(k), t1);
+    const uint32_t bytes = static_cast<uint32_t>(t1 - row0) * ROW;
+    const BufferRsrc rk = make_rsrc(kbase + static_cast<int64_t>(row0) * ROW, bytes);
+    const BufferRsrc rv = make_rsrc(vbase + static_cast<int64_t>(row0) * ROW, bytes);
+    if constexpr (KW == 2) {
+      const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(rk, koff, 0, 0);
+      r.k[0] = x.x;
+      r.k[1] = x.y;
+    } else {
+#pragma unroll
+      for (int q = 0; q < KW / 4; ++q) {
+        const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 16 * q, 0, 0);
+        r.k[4 * q] = x.x;
+        r.k[4 * q + 1] = x.y;
+        r.k[4 * q + 2] = x.z;
+        r.k[4 * q + 3] = x.w;
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+      for (int q = 0; q < VW; ++q) r.v[rr][q] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + rr * ROW + 64 * q, 0, 0);
+  };
+
+  // ---- set-up loads first (centroids, query, signs, appended token), then
+  // the first tiles' rows: vector loads return in order, so a set-up value
+  // requested after the rows would wait for them.
+  const float* cent_t = tid < 256 ? a.cent_k : a.cent_v;  // thread t stages entry t & 255 of table t / 256
+  const float ce0 = cent_t[tid & 15], ce1 = cent_t[(tid >> 4) & 15];
+  const int sh_k = table_shift(a.cent_k), sh_v = table_shift(a.cent_v);
+  const bool appending = a.new_k != nullptr;
+  const bool appender = appending && split == 0 && wave < 2;
+  constexpr int kLevels = 15;
+  float tok[E], bnd[kLevels];
+  if (appender) {
+    const int64_t toff = static_cast<int64_t>(lkv) * D + lane * E;
+    const void* src = wave == 0 ? a.new_k : a.new_v;
+#pragma unroll
+    for (int i = 0; i < E; ++i)
+      tok[i] = a.new_f16 ? __half2float(static_cast<const __half*>(src)[toff + i]) : static_cast<const float*>(src)[toff + i];
+    const float* b = wave == 0 ? a.bnd_k : a.bnd_v;
+#pragma unroll
+    for (int k = 0; k < kLevels; ++k) bnd[k] = b[k];
+  }
+  float qe[E], sg_first[E], sg_second[E];
+  if (wave < 4) {
+    const int64_t qoff = (static_cast<int64_t>(layer) * a.query_heads + qh0 + wave) * D + lane * E;
+#pragma unroll
+    for (int i = 0; i < E; ++i)
+      qe[i] = QF16 ? __half2float(static_cast<const __half*>(a.q)[qoff + i]) : static_cast<const float*>(a.q)[qoff + i];
+  }
+  if ((wave < 4 && (a.rotate_query || a.inverse_output)) || appender) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      sg_first[i] = a.signs_right[lane * E + i];
+      sg_second[i] = a.signs_left[lane * E + i];
+    }
+  }
+
+  constexpr int NR = kPrefetch + 1;
+  Raw ring[NR];
+  int kq[NR];  // tile held by each ring slot (wavefront-uniform)
+#pragma unroll
+  for (int j = 0; j < kPrefetch; ++j) {
+    kq[j] = j * kWaves + wave;
+    load_tile(kq[j], ring[j]);
+  }
+  int* s_claim = reinterpret_cast<int*>(s_misc + 8);
+  if (tid == 0) *s_claim = kPrefetch * kWaves;  // first dynamic claim; read only after the set-up barriers
+  // lane 0 takes the next tile; the value is read (readfirstlane) only where
+  // the tile is loaded, one iteration later, so the atomic's latency hides
+  auto claim = [&]() {
+    int k = 0;
+    if (lane == 0) k = atomicAdd(s_claim, 1);
+    return k;
+  };
+
+  uint2* s_stage = reinterpret_cast<uint2*>(smem + L::kStage);  // [2][256]
+  s_stage[tid] = table_entry(ce0, ce1, tid < 256 ? sh_k : sh_v);
+
+  // ---- append mode: rotate (as on append) and quantize the new token.
+  if (appender) {
+    if (wave == 1 ? a.rotate_new_v : a.rotate_new_k) wave_rotate_signs<D>(tok, sg_first, sg_second, a.sqrt_d);
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const uint32_t code = quantize_count<4>(tok[i], bnd);
+      s_codes[wave * D + lane * E + i] = static_cast<uint8_t>(code);
+      s_cur[wave * D + lane * E + i] = (wave == 0 ? a.cent_k : a.cent_v)[code];
+    }
+  }
+
+  // ---- queries: optional rotation (bit-identical to the reference), the
+  // softmax scale and log2(e) folded in (scores come out in log2 units), then
+  // the exact f16 split of q * 2^shift.
+  if (wave < 4) {
+    if (a.rotate_query) wave_rotate_signs<D>(qe, sg_first, sg_second, a.sqrt_d);
+    float mxq = 0.f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      qe[i] *= a.q_scale;
+      s_q[wave * D + lane * E + i] = qe[i];
+      mxq = fmaxf(mxq, fabsf(qe[i]));
+    }
+    mxq = group_reduce<kWave, OpMax>(mxq);
+    const int sh_q = scale_shift(mxq);
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const float x = ldexpf(qe[i], sh_q);
+      const _Float16 h = static_cast<_Float16>(x);
+      const _Float16 l = static_cast<_Float16>(x - static_cast<float>(h));
+      s_qb[wave * L::kQbStride + lane * E + i] = __builtin_bit_cast(uint16_t, h);
+      s_qb[(4 + wave) * L::kQbStride + lane * E + i] = __builtin_bit_cast(uint16_t, l);
+    }
+    if (lane == 0) s_misc[wave] = ldexpf(1.f, -(sh_q + sh_k));  // raw score -> log2 units
+  }
+  __syncthreads();
+  replicate_tables(smem, s_stage, wave, lane);
+  __syncthreads();
+  if (appender) {
+    constexpr int W = D * 4 / 32;
+    if (hg == 0 && lane < W) {
+      uint32_t* dst = (wave == 0 ? a.k_slab : a.v_slab) + (static_cast<int64_t>(lkv) * a.cap + a.seq_len) * W + lane;
+      *dst = pack_word<4, D>(s_codes + wave * D, lane);
+    }
+  }
+
+  // ---- this lane's query operands: column n (hi split of head n, lo split
+  // of head n - 4, zero from 8), the g-th quarter of the dims; each pair of
+  // dims fills the k-slots of both key parts (hi, lo).
+  uint32_t qd[D / 8];  // f16 pairs of this lane's D / 4 dims
+#pragma unroll
+  for (int i = 0; i < D / 8; ++i)
+    qd[i] = n < 8 ? reinterpret_cast<const uint32_t*>(s_qb + n * L::kQbStride + g * (D / 4))[i] : 0u;
+  const float score_scale = s_misc[n & 3];
+  const float out_scale = ldexpf(1.f, -(sh_v + 7));  // weights carry 2^7, values 2^sh_v
+
+  // table bases (offsets into smem): copy lane % 32, key table at 0, value
+  // table at 65536; bits 8..15 stay clear for the code byte
+  const uint32_t base_k = (lane & 31) * 8;
+  const uint32_t base_v = base_k + kTableBytes;
+
+  // Softmax state, log2 units.  m_lane: running maximum of head n % 4
+  // (wavefront-wide: every lane sharing lane % 4 holds the same value).
+  // bias: 7 - m_lane on lanes n < 4 (the weights come out as p * 2^7, the
+  // scale of their exact f16 split), -inf elsewhere, so that the other lanes'
+  // weights are exp2(-inf) = 0 with no mask.  l_lane: this lane's softmax sum
+  // in units of 2^-7 (lanes n < 4).
+  const bool head_lane = n < 4;
+  float m_lane = -INFINITY;
+  float bias = head_lane ? INFINITY : -INFINITY;  // +inf forces a maximum on the first tile
+  float l_lane = 0.f;
+  f32x4v acc[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) acc[j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  constexpr float kWeightExp = 7.f;  // weights carry 2^7
+
+  // Per tile: key lookups (KB table reads), score products, softmax, value
+  // lookups (NV x 2 table reads), value products.  Software-pipelined over the
+  // tiles so that table reads and products of neighbouring tiles overlap with
+  // one set of lookup registers: iteration i runs
+  //   key lookups(i + 1), softmax + value products(i), value lookups(i + 1),
+  //   score products(i + 1)
+  // (the key reads have the softmax and value products to land, the value
+  // reads the score products and the next iteration's first half).
+  uint2 kl[KB];      // key lookups, one per byte of the lane's quarter row
+  uint2 vl[NV][2];   // value lookups: product j, token pair (0, 1) / (2, 3)
+  auto key_lookups = [&](const Raw& r) {
+#pragma unroll
+    for (int b = 0; b < KB; ++b) kl[b] = lds_read_u2(smem, lut_addr_dyn(r.k[b / 4], base_k, b & 3));
+  };
+  auto value_lookups = [&](const Raw& r) {
+#pragma unroll
+    for (int q = 0; q < VW; ++q) {
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        uint32_t w0 = r.v[2 * pr][q], w1 = r.v[2 * pr + 1][q];
+        if constexpr (D == 64) {
+          w0 = (n & 1) ? (w0 >> 16) : (w0 & 0xffffu);
+          w1 = (n & 1) ? (w1 >> 16) : (w1 & 0xffffu);
+        }
+        // nibbles of one dim in two tokens interleaved into one byte
+        const uint32_t ev = (w0 & 0x0f0f0f0fu) | ((w1 << 4) & 0xf0f0f0f0u);
+        const uint32_t od = ((w0 >> 4) & 0x0f0f0f0fu) | (w1 & 0xf0f0f0f0u);
+        constexpr int JN = D == 64 ? 4 : 8;  // dims per dword this lane uses
+#pragma unroll
+        for (int jj = 0; jj < JN; ++jj)
+          vl[q * 8 + jj][pr] = lds_read_u2(smem, lut_addr_dyn((jj & 1) ? od : ev, base_v, jj >> 1));
+      }
+    }
+  };
+  auto scores = [&](f32x4v& ds) {
+    ds = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) {
+      const f16x8 A = as_f16x8(kl[2 * s2].x, kl[2 * s2].y, kl[2 * s2 + 1].x, kl[2 * s2 + 1].y);
+      const f16x8 B = as_f16x8(qd[2 * s2], qd[2 * s2], qd[2 * s2 + 1], qd[2 * s2 + 1]);
+      ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, ds, 0, 0, 0);
+    }
+  };
+  // Softmax and value products of tile k.  Lanes n < 4 hold head n's scores
+  // of tokens 4g + rr once column n + 4 (the query's lo split) is added; the
+  // other lanes' weights are zero through `bias`.  Only a split's last tiles
+  // can be partial: their rows past the end get weight zero.
+  auto values = [&](const f32x4v& ds, int k) {
+    float sc[4], z[4];
+    const int row0 = tile_row(k);
+    const bool full = row0 + kTile <= t1;  // wavefront-uniform
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      sc[rr] = ds[rr] + dpp_move<kDppRor12>(ds[rr]);  // column n + column n + 4
+      z[rr] = fmaf(sc[rr], score_scale, bias);
+    }
+    if (!full) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) z[rr] = row0 + 4 * g + rr < t1 ? z[rr] : -INFINITY;
+    }
+    const bool need = z[0] > kRescaleThreshold + kWeightExp || z[1] > kRescaleThreshold + kWeightExp ||
+                      z[2] > kRescaleThreshold + kWeightExp || z[3] > kRescaleThreshold + kWeightExp;
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      // a running maximum moves: wavefront-wide per head (lanes sharing
+      // lane % 4), accumulators of head rr (rows rr, 4 + rr) rescaled
+      float mx = -INFINITY;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) mx = head_lane && row0 + 4 * g + rr < t1 ? fmaxf(mx, sc[rr] * score_scale) : mx;
+      mx = strided_reduce<4, OpMax>(mx);
+      float alpha = 1.f;
+      if (mx > m_lane + kRescaleThreshold) {
+        alpha = fast_exp2(m_lane - mx);  // 0 before the first maximum
+        m_lane = mx;
+      }
+      l_lane *= alpha;
+      bias = head_lane ? kWeightExp - m_lane : -INFINITY;
+      const f32x4v al = {quad_broadcast_t<0>(alpha), quad_broadcast_t<1>(alpha), quad_broadcast_t<2>(alpha),
+                         quad_broadcast_t<3>(alpha)};
+#pragma unroll
+      for (int j = 0; j < NV; ++j) acc[j] *= al;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) z[rr] = row0 + 4 * g + rr < t1 ? fmaf(sc[rr], score_scale, bias) : -INFINITY;
+    }
+    float p[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      p[rr] = fast_exp2(z[rr]);  // p * 2^7
+      l_lane += p[rr];
+    }
+    // exact split of p * 2^7: hi = low 13 mantissa bits cleared, lo = rest
+    uint32_t wh[2];
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+      const float x0 = p[2 * pr], x1 = p[2 * pr + 1];
+      const float h0 = __uint_as_float(__float_as_uint(x0) & 0xffffe000u);
+      const float h1 = __uint_as_float(__float_as_uint(x1) & 0xffffe000u);
+      wh[pr] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(h0, h1));
+      const uint32_t wl = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0 - h0, x1 - h1));
+      // rows 4..7 (lanes n = 4..7) take the lo split of head n - 4: row_shr:4, bank 1 only
+      wh[pr] = static_cast<uint32_t>(
+          __builtin_amdgcn_update_dpp(static_cast<int>(wh[pr]), static_cast<int>(wl), 0x114, 0xf, 0x2, false));
+    }
+    const f16x8 Aw = as_f16x8(wh[0], wh[0], wh[1], wh[1]);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const f16x8 B = as_f16x8(vl[j][0].x, vl[j][0].y, vl[j][1].x, vl[j][1].y);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aw, B, acc[j], 0, 0, 0);
+    }
+  };
+
+  // Claims past the split's end load nothing and read as masked tiles; a
+  // wavefront's claims only grow, so it stops at its first such tile.  The
+  // stages of a tile run in order; the three wavefronts of a SIMD overlap
+  // each other's table-read and product latencies.
+  bool more = kq[0] < n_tiles;
+  int claimed = claim();
+  while (more) {
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      const int nx = (j + kPrefetch) % NR;
+      kq[nx] = __builtin_amdgcn_readfirstlane(claimed);
+      load_tile(kq[nx], ring[nx]);
+      claimed = claim();
+      f32x4v ds;
+      key_lookups(ring[j]);
+      scores(ds);
+      value_lookups(ring[j]);
+      values(ds, kq[j]);
+      if (kq[(j + 1) % NR] >= n_tiles) {
+        more = false;
+        break;
+      }
+    }
+  }
+
+  // ---- combine: rows h and 4 + h (lane groups 0 and 1), then the
+  // wavefronts.  Lane n of group 0 holds head rr's output at dims of column n.
+  __syncthreads();  // the tables are dead: reuse their space
+  float* s_red = reinterpret_cast<float*>(smem);                  // [kWaves][4][D]
+  float* s_mw = reinterpret_cast<float*>(smem + kWaves * 4 * D * 4);  // [kWaves][4]
+  float* s_lw = s_mw + kWaves * 4;                                 // [kWaves][4]
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    // dim of column n in product j: 8n + j (D = 128), 8n + j and 128 + 8n + j - 8 (D = 256), 4n + j (D = 64)
+    const int dim = D == 64 ? 4 * n + j : (j < 8 ? 8 * n + j : 128 + 8 * n + (j - 8));
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const float v = xor_reduce<16, OpSum>(acc[j][rr]);
+      if (g == 0) s_red[(wave * 4 + rr) * D + dim] = v * out_scale;
+    }
+  }
+  {
+    const float lw = xor_reduce<32, OpSum>(xor_reduce<16, OpSum>(head_lane ? l_lane : 0.f)) * (1.f / 128.f);
+    if (lane < 4) {
+      s_mw[wave * 4 + lane] = m_lane;
+      s_lw[wave * 4 + lane] = lw;
+    }
+  }
+  __syncthreads();
+
+  auto wave_weights = [&](int h, float (&f)[kWaves]) {
+    float M = s_mw[h];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_mw[w * 4 + h]);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) f[w] = s_mw[w * 4 + h] == -INFINITY ? 0.f : fast_exp2(s_mw[w * 4 + h] - M);
+    return M;
+  };
+  const int64_t qhg0 = static_cast<int64_t>(layer) * a.query_heads + qh0;
+  if (wave < 4) {
+    float f[kWaves];
+    const float M = wave_weights(wave, f);
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) l = fmaf(s_lw[w * 4 + wave], f[w], l);
+    float e[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) v = fmaf(s_red[(w * 4 + wave) * D + lane * E + i], f[w], v);
+      e[i] = v;
+    }
+    if (a.n_splits == 1) {
+      // one split: finish the row here (current token, normalisation, inverse rotation)
+      float* row = s_red + wave * D;  // wavefront `wave` owns this row of the first block now
+#pragma unroll
+      for (int i = 0; i < E; ++i) row[lane * E + i] = e[i];
+      const float* ck = appending ? s_cur : a.cur_k ? a.cur_k + static_cast<int64_t>(lkv) * D : nullptr;
+      const float* cv = appending ? s_cur + D : a.cur_v ? a.cur_v + static_cast<int64_t>(lkv) * D : nullptr;
+      finish_row<D>(row, M, l, s_q + wave * D, ck, cv, a.inverse_output, sg_second, sg_first, a.sqrt_d,
+                    a.out + (qhg0 + wave) * D);
+    } else {
+      // several splits: publish this split's (max, sum, accumulator rotated back)
+      if (a.inverse_output) wave_rotate_signs<D>(e, sg_second, sg_first, a.sqrt_d);
+      float* dst = a.ws_acc + ((qhg0 + wave) * a.n_splits + split) * D + lane * E;
+#pragma unroll
+      for (int i = 0; i < E; ++i) dst[i] = e[i];
+      if (lane == 0) {
+        a.ws_ml[((qhg0 + wave) * a.n_splits + split) * 2] = M;
+        a.ws_ml[((qhg0 + wave) * a.n_splits + split) * 2 + 1] = l;
+      }
+      if (split == 0 && (appending || a.cur_k != nullptr)) {
+        const float* ck = (appending ? s_cur : a.cur_k + static_cast<int64_t>(lkv) * D) + lane * E;
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < E; ++i) dot = fmaf(s_q[wave * D + lane * E + i], ck[i], dot);
+        dot = group_sum<kWave>(dot);
+        if (lane == 0) a.ws_cur_s[qhg0 + wave] = dot;
+        if (wave == 0 && hg == 0) {
+          float v[E];
+          const float* cv = (appending ? s_cur + D : a.cur_v + static_cast<int64_t>(lkv) * D) + lane * E;
+#pragma unroll
+          for (int i = 0; i < E; ++i) v[i] = cv[i];
+          if (a.inverse_output) wave_rotate_signs<D>(v, sg_second, sg_first, a.sqrt_d);
+#pragma unroll
+          for (int i = 0; i < E; ++i) a.ws_cur_v[static_cast<int64_t>(lkv) * D + lane * E + i] = v[i];
+        }
+      }
+    }
+  }
+}

@@ -985,6 +985,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   }
 }
 
+#include "decode_mx.hpp"
+
 // Log-sum-exp merge of the splits: M = max(max_s M_s, current score),
 // L = sum_s L_s 2^(M_s - M) (+ 2^(score - M)), out = (sum_s A_s 2^(M_s - M)
 // (+ 2^(score - M) value)) / L.  The split accumulators A_s are already
@@ -1188,15 +1190,24 @@ int pick_hg(int group) {
   return 1;
 }
 
+// The split kernel a decode call runs: the float32 kernel (decode_kernel,
+// 4x4x1 fp32 matrix products or VALU FMAs, 256 threads, two workgroups per
+// CU) or, for 4-bit packed rows in groups of 4 query heads at head_dim 64 or
+// 128, decode_mx_kernel (16x16x32 products of exact f16 splits, 512 threads,
+// one workgroup per CU) unless TQ_F32_PRODUCTS asks for the former.
+enum class SplitKernel { Fp32, Mx };
+
 struct Plan {
   int hg, n_hgroups, units, n_splits;
+  SplitKernel kernel;
+  int block_rows;  // rows per workgroup iteration (the unit the sequence is dealt out in)
 };
 
 constexpr int kMinTokensPerSplit = 128;
 
-int default_splits(int units, int64_t seq_len, int num_cus) {
+int default_splits(int units, int64_t seq_len, int num_cus, int wgs_per_cu) {
   if (num_cus <= 0) num_cus = 256;
-  const int64_t target = 2LL * num_cus;  // two workgroups per CU
+  const int64_t target = static_cast<int64_t>(wgs_per_cu) * num_cus;
   int64_t ns = (target + units - 1) / units;
   const int64_t by_len = std::max<int64_t>(1, (seq_len + kMinTokensPerSplit - 1) / kMinTokensPerSplit);
   ns = std::min(ns, by_len);
@@ -1272,10 +1283,26 @@ void* device_scratch() {
   return g_scratch_ptr[dev];
 }
 
-// Fills the split plan.  block_rows: rows per workgroup iteration of the
-// kernel that will run (the unit the sequence is dealt out in); every split
-// gets at least one block.
-int make_plan(int num_layers, int kv_heads, int query_heads, int64_t seq_len, int n_splits, int block_rows, Plan* p) {
+// Rows per workgroup iteration of decode_kernel for `fmt` (2/3/4 packed
+// bits, 16 dense fp16, 32 dense fp32): tokens per lane group x lane groups
+// per wavefront (64 / (D / slice dims)) x wavefronts; packed slices hold 16
+// dimensions, fp16 rows 8, fp32 rows 4.
+int decode_block_rows(int fmt, int head_dim) {
+  const bool packed = fmt == 2 || fmt == 3 || fmt == 4;
+  const int slice_dims = packed ? 16 : (fmt == 16 ? 8 : 4);
+  return kTokensPerIter * kWavesPerBlock * kWave * slice_dims / head_dim;
+}
+
+SplitKernel pick_kernel(int fmt, int head_dim, int hg, int flags) {
+  if (fmt == 4 && hg == 4 && (head_dim == 64 || head_dim == 128) && (flags & TQ_F32_PRODUCTS) == 0)
+    return SplitKernel::Mx;
+  return SplitKernel::Fp32;
+}
+
+// Fills the split plan of a decode call over `fmt` rows (see
+// decode_block_rows) with decode `flags`; every split gets at least one block.
+int make_plan(int num_layers, int kv_heads, int query_heads, int64_t seq_len, int n_splits, int fmt, int head_dim,
+              int flags, Plan* p) {
   if (num_layers <= 0 || kv_heads <= 0 || query_heads <= 0)
     return fail(TQ_ERR_BAD_ARG, "num_layers, kv_heads and query_heads must be positive");
   if (query_heads % kv_heads != 0)
@@ -1291,21 +1318,14 @@ int make_plan(int num_layers, int kv_heads, int query_heads, int64_t seq_len, in
   if (units > max_wg)
     return fail(TQ_ERR_BAD_ARG, "num_layers x kv_heads x head groups exceeds one launch; decode fewer layers per call");
   p->units = static_cast<int>(units);
-  int ns = n_splits > 0 ? n_splits : default_splits(p->units, seq_len, device_cu_count());
+  p->kernel = pick_kernel(fmt, head_dim, p->hg, flags);
+  p->block_rows = p->kernel == SplitKernel::Mx ? mx::kStride : decode_block_rows(fmt, head_dim);
+  const int wgs_per_cu = p->kernel == SplitKernel::Mx ? 1 : 2;
+  int ns = n_splits > 0 ? n_splits : default_splits(p->units, seq_len, device_cu_count(), wgs_per_cu);
   if (ns > kMaxSplits) return fail(TQ_ERR_BAD_ARG, "n_splits must be at most " + std::to_string(kMaxSplits));
-  const int64_t blocks = std::max<int64_t>(1, (seq_len + block_rows - 1) / block_rows);
+  const int64_t blocks = std::max<int64_t>(1, (seq_len + p->block_rows - 1) / p->block_rows);
   p->n_splits = static_cast<int>(std::min<int64_t>({blocks, static_cast<int64_t>(ns), max_wg / units}));
   return TQ_OK;
-}
-
-// Rows per workgroup iteration of the decode kernel for `fmt` (2/3/4 packed
-// bits, 16 dense fp16, 32 dense fp32): tokens per lane group x lane groups
-// per wavefront (64 / (D / slice dims)) x wavefronts; packed slices hold 16
-// dimensions, fp16 rows 8, fp32 rows 4.
-int decode_block_rows(int fmt, int head_dim) {
-  const bool packed = fmt == 2 || fmt == 3 || fmt == 4;
-  const int slice_dims = packed ? 16 : (fmt == 16 ? 8 : 4);
-  return kTokensPerIter * kWavesPerBlock * kWave * slice_dims / head_dim;
 }
 
 template <class Fmt, int D, int HG, bool QF16, bool SC>
@@ -1379,6 +1399,39 @@ struct AppendSpec {
   int flags;  // TQ_ROTATE_KEYS | TQ_ROTATE_VALUES
 };
 
+int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hipStream_t stream, hipEvent_t start,
+                hipEvent_t stop);
+int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream);
+
+template <int D, bool QF16>
+void launch_mx_t(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  if (start != nullptr || stop != nullptr)
+    hipExtLaunchKernelGGL((decode_mx_kernel<D, QF16>), dim3(nblk), dim3(mx::kThreads), 0, stream, start, stop, 0, a);
+  else
+    hipLaunchKernelGGL((decode_mx_kernel<D, QF16>), dim3(nblk), dim3(mx::kThreads), 0, stream, a);
+}
+
+template <int D>
+void launch_mx_d(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  if (a.q_f16)
+    launch_mx_t<D, true>(a, nblk, stream, start, stop);
+  else
+    launch_mx_t<D, false>(a, nblk, stream, start, stop);
+}
+
+int launch_mx(const DecodeArgs& a, int head_dim, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  switch (head_dim) {
+    case 64:
+      launch_mx_d<64>(a, nblk, stream, start, stop);
+      return TQ_OK;
+    case 128:
+      launch_mx_d<128>(a, nblk, stream, start, stop);
+      return TQ_OK;
+    default:
+      return fail(TQ_ERR_UNSUPPORTED, "decode_mx_kernel: unsupported head dimension " + std::to_string(head_dim));
+  }
+}
+
 int decode_common(int fmt, const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
                   int head_dim, const void* keys, const void* values, int64_t capacity, int64_t seq_len,
                   const float* cent_k, const float* cent_v, const float* signs_left, const float* signs_right,
@@ -1419,7 +1472,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   if (capacity * row_bytes >= (1LL << 31))
     return fail(TQ_ERR_BAD_ARG, "capacity * row bytes must stay below 2 GiB per (layer, KV head)");
   Plan p;
-  rc = make_plan(num_layers, kv_heads, query_heads, seq_len, n_splits, decode_block_rows(fmt, head_dim), &p);
+  rc = make_plan(num_layers, kv_heads, query_heads, seq_len, n_splits, fmt, head_dim, flags, &p);
   if (rc) return rc;
   if (p.n_splits > 1 &&
       static_cast<int64_t>(num_layers) * query_heads * (head_dim / kMergeDims) > ((int64_t(1) << 32) - 1) / kBlock)
@@ -1486,28 +1539,43 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   m.cur_v = a.ws_cur_v;
   m.out = out;
 
-  switch (fmt) {
-    case 2:
-      rc = dispatch_d<PackedB2>(a, head_dim, p.hg, nblk, stream, start, stop);
-      break;
-    case 3:
-      rc = dispatch_d<PackedB3>(a, head_dim, p.hg, nblk, stream, start, stop);
-      break;
-    case 4:
-      rc = dispatch_d<PackedB4>(a, head_dim, p.hg, nblk, stream, start, stop);
-      break;
-    case 16:
-      rc = dispatch_d<DenseF16>(a, head_dim, p.hg, nblk, stream, start, stop);
-      break;
-    case 32:
-      rc = dispatch_d<DenseF32>(a, head_dim, p.hg, nblk, stream, start, stop);
-      break;
-    default:
-      return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(fmt));
+  if (p.kernel == SplitKernel::Mx) {
+    rc = launch_mx(a, head_dim, nblk, stream, start, stop);
+  } else {
+    rc = launch_fp32(a, fmt, head_dim, p.hg, nblk, stream, start, stop);
   }
   if (rc) return rc;
   rc = launch_status("decode_kernel");
   if (rc || p.n_splits == 1) return rc;
+  return launch_merge(m, num_layers, query_heads, head_dim, stream);
+}
+
+int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hipStream_t stream, hipEvent_t start,
+                hipEvent_t stop) {
+  int rc;
+  switch (fmt) {
+    case 2:
+      rc = dispatch_d<PackedB2>(a, head_dim, hg, nblk, stream, start, stop);
+      break;
+    case 3:
+      rc = dispatch_d<PackedB3>(a, head_dim, hg, nblk, stream, start, stop);
+      break;
+    case 4:
+      rc = dispatch_d<PackedB4>(a, head_dim, hg, nblk, stream, start, stop);
+      break;
+    case 16:
+      rc = dispatch_d<DenseF16>(a, head_dim, hg, nblk, stream, start, stop);
+      break;
+    case 32:
+      rc = dispatch_d<DenseF32>(a, head_dim, hg, nblk, stream, start, stop);
+      break;
+    default:
+      return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(fmt));
+  }
+  return rc;
+}
+
+int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream) {
   const unsigned mblk =
       static_cast<unsigned>(static_cast<int64_t>(num_layers) * query_heads * (head_dim / kMergeDims));
   switch (head_dim) {
@@ -1937,15 +2005,15 @@ int tq_unpack_dequantize_scaled(const uint32_t* codes, const float* scales, int6
   return unpack_impl(codes, groups, capacity, seq_len, head_dim, bits, centroids, scales, out, stream);
 }
 
-int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int head_dim, int64_t seq_len,
-                             int num_cus) {
+int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int head_dim, int bits, int flags,
+                             int64_t seq_len, int num_cus) {
   if (num_layers <= 0 || kv_heads <= 0 || query_heads <= 0 || query_heads % kv_heads != 0)
     return fail(TQ_ERR_BAD_ARG, "bad head configuration");
-  (void)head_dim;
   const int group = query_heads / kv_heads;
   const int hg = pick_hg(group);
   const int units = num_layers * kv_heads * (group / hg);
-  return default_splits(units, seq_len, num_cus);
+  const bool mx_kernel = pick_kernel(bits, head_dim, hg, flags) == SplitKernel::Mx;
+  return default_splits(units, seq_len, num_cus, mx_kernel ? 1 : 2);
 }
 
 size_t tq_decode_workspace_bytes(int num_layers, int kv_heads, int query_heads, int head_dim, int n_splits,
@@ -1956,7 +2024,8 @@ size_t tq_decode_workspace_bytes(int num_layers, int kv_heads, int query_heads, 
   const int hg = pick_hg(group);
   const int units = num_layers * kv_heads * (group / hg);
   int ns = n_splits;
-  if (ns <= 0) ns = default_splits(units, static_cast<int64_t>(kMaxSplits) * kMinTokensPerSplit, num_cus);
+  // the larger of the two split kernels' defaults (two workgroups per CU)
+  if (ns <= 0) ns = default_splits(units, static_cast<int64_t>(kMaxSplits) * kMinTokensPerSplit, num_cus, 2);
   ns = std::min(ns, kMaxSplits);
   return workspace_layout(static_cast<int64_t>(num_layers) * query_heads, static_cast<int64_t>(num_layers) * kv_heads,
                           head_dim, ns)
@@ -1985,7 +2054,7 @@ int tq_decode_noalloc(const void* query, int query_dtype, int num_layers, int qu
   // The split plan this call resolves to, and the scratch it needs, before
   // anything touches the device.
   Plan p;
-  rc = make_plan(num_layers, kv_heads, query_heads, seq_len, n_splits, decode_block_rows(bits, head_dim), &p);
+  rc = make_plan(num_layers, kv_heads, query_heads, seq_len, n_splits, bits, head_dim, flags, &p);
   if (rc) return rc;
   const size_t need = workspace_layout(static_cast<int64_t>(num_layers) * query_heads,
                                        static_cast<int64_t>(num_layers) * kv_heads, head_dim, p.n_splits)
@@ -2024,10 +2093,12 @@ int tq_decode_scaled_timed(const void* query, int query_dtype, int num_layers, i
   if (!valid_bits(bits)) return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
   if (seq_len > 0 && (key_scales == nullptr || value_scales == nullptr))
     return fail(TQ_ERR_BAD_ARG, "key_scales and value_scales must be non-null");
+  // Per-vector scales multiply the softmax weights, which the f16-split
+  // kernel cannot hold for a factor of unknown size: always float32 products.
   return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes, value_codes,
-                       capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, flags,
-                       current_keys, current_values, n_splits, workspace, workspace_bytes, out, stream, start, stop,
-                       nullptr,
+                       capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right,
+                       flags | TQ_F32_PRODUCTS, current_keys, current_values, n_splits, workspace, workspace_bytes,
+                       out, stream, start, stop, nullptr,
                        seq_len > 0 ? key_scales : nullptr, seq_len > 0 ? value_scales : nullptr);
 }
 

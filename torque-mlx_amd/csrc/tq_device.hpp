@@ -43,8 +43,9 @@ constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;   // lane i <-> 7 - i within 8
 constexpr int kDppMirror = 0x140;       // lane i <-> 15 - i within 16
-constexpr int kDppRor4 = 0x124;         // lane i <- lane (i + 4) mod 16
+constexpr int kDppRor4 = 0x124;         // lane i <- lane (i - 4) mod 16 (rotate right: data moves up)
 constexpr int kDppRor8 = 0x128;         // lane i <- lane (i + 8) mod 16, i.e. i xor 8
+constexpr int kDppRor12 = 0x12C;        // lane i <- lane (i + 4) mod 16
 
 // gfx950 v_permlane16_swap / v_permlane32_swap.  With x in the first operand
 // and y in the second, for every lane pair (i, i xor M), M = 16 or 32, i the

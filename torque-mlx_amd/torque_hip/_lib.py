@@ -33,6 +33,7 @@ TQ_ROTATE_KEYS = 1
 TQ_ROTATE_VALUES = 2
 TQ_ROTATE_QUERY = 1
 TQ_INVERSE_OUTPUT = 2
+TQ_F32_PRODUCTS = 4
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -52,7 +53,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tq_quantize_dequantize_scaled": (_i, [_p, _p, _i, _i64, _i, _i, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p]),
     "tq_unpack_dequantize": (_i, [_p, _i64, _i64, _i64, _i, _i, _p, _p, _p]),
     "tq_unpack_dequantize_scaled": (_i, [_p, _p, _i64, _i64, _i64, _i, _i, _p, _p, _p]),
-    "tq_decode_default_splits": (_i, [_i, _i, _i, _i, _i64, _i]),
+    "tq_decode_default_splits": (_i, [_i, _i, _i, _i, _i, _i, _i64, _i]),
     "tq_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "tq_decode": (
         _i,

@@ -69,8 +69,21 @@ def num_cus(dev: torch.device) -> int:
     return int(torch.cuda.get_device_properties(dev).multi_processor_count)
 
 
-def plan_splits(num_layers: int, kv_heads: int, query_heads: int, head_dim: int, seq_len: int, dev: torch.device) -> int:
-    return _lib.call("tq_decode_default_splits", num_layers, kv_heads, query_heads, head_dim, seq_len, num_cus(dev))
+def plan_splits(
+    num_layers: int,
+    kv_heads: int,
+    query_heads: int,
+    head_dim: int,
+    seq_len: int,
+    dev: torch.device,
+    *,
+    bit_width: int = 0,
+    flags: int = 0,
+) -> int:
+    """The library's default split count for a decode over ``bit_width``-bit rows (0: dense rows)."""
+    return _lib.call(
+        "tq_decode_default_splits", num_layers, kv_heads, query_heads, head_dim, bit_width, flags, seq_len, num_cus(dev)
+    )
 
 
 def workspace_for(num_layers: int, kv_heads: int, query_heads: int, head_dim: int, n_splits: int, dev: torch.device) -> torch.Tensor:
@@ -102,20 +115,26 @@ def packed_decode(
     out: torch.Tensor | None = None,
     key_scales: torch.Tensor | None = None,
     value_scales: torch.Tensor | None = None,
+    f32_products: bool = False,
 ) -> torch.Tensor:
     """One ``tq_decode`` launch on device tensors; returns out[L, Hq, D] float32.
 
     With ``key_scales`` / ``value_scales`` ([L, Hkv, capacity] float32, slabs
     written by ``tq_append_scaled``) the launch is ``tq_decode_scaled``.
+    ``f32_products`` selects the float32-product split kernel (TQ_F32_PRODUCTS)
+    where the float16-split matrix kernel would run; scaled decodes always
+    take it (the library adds the flag), so their split plan does too.
     """
     dev = query.device
+    scaled = key_scales is not None or value_scales is not None
+    flags = (_lib.TQ_ROTATE_QUERY if rotate_query else 0) | (_lib.TQ_INVERSE_OUTPUT if inverse_output else 0)
+    flags |= _lib.TQ_F32_PRODUCTS if f32_products or scaled else 0
     if n_splits is None or n_splits <= 0:
-        n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev)
+        n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev, bit_width=bit_width,
+                               flags=flags)
     ws = workspace_for(num_layers, kv_heads, query_heads, head_dim, n_splits, dev)
     if out is None:
         out = torch.empty((num_layers, query_heads, head_dim), dtype=torch.float32, device=dev)
-    flags = (_lib.TQ_ROTATE_QUERY if rotate_query else 0) | (_lib.TQ_INVERSE_OUTPUT if inverse_output else 0)
-    scaled = key_scales is not None or value_scales is not None
     if scaled and (key_scales is None or value_scales is None):
         raise ValueError("key_scales and value_scales must both be given or both be None")
     scale_args = (key_scales.data_ptr(), value_scales.data_ptr()) if scaled else ()
@@ -182,13 +201,14 @@ def packed_decode_append(
     if new_keys.dtype != new_values.dtype:
         raise ValueError("new_keys and new_values must share one dtype")
     dev = query.device
+    append_flags = (_lib.TQ_ROTATE_KEYS if rotate_keys else 0) | (_lib.TQ_ROTATE_VALUES if rotate_values else 0)
+    decode_flags = (_lib.TQ_ROTATE_QUERY if rotate_query else 0) | (_lib.TQ_INVERSE_OUTPUT if inverse_output else 0)
     if n_splits is None or n_splits <= 0:
-        n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev)
+        n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev, bit_width=bit_width,
+                               flags=decode_flags)
     ws = workspace_for(num_layers, kv_heads, query_heads, head_dim, n_splits, dev)
     if out is None:
         out = torch.empty((num_layers, query_heads, head_dim), dtype=torch.float32, device=dev)
-    append_flags = (_lib.TQ_ROTATE_KEYS if rotate_keys else 0) | (_lib.TQ_ROTATE_VALUES if rotate_values else 0)
-    decode_flags = (_lib.TQ_ROTATE_QUERY if rotate_query else 0) | (_lib.TQ_INVERSE_OUTPUT if inverse_output else 0)
     _lib.call(
         "tq_decode_append",
         query.data_ptr(),
