@@ -39,13 +39,17 @@
 //   its row), so lanes n < 4 end up with
 //   head n's scores of their 4 tokens.
 //
+//   Softmax: the four score registers are spread over the 16 lanes of a
+//   row (DPP moves), so that lane m holds head m % 4's score of token
+//   4g + m / 4 % 4 and every exp2 is a useful one.
+//
 //   Values, O[row][dim] += P[row][k] * V[k][dim]: B = value codes, lane
 //   (n, g) reading dword n (8 dims) of rows 4g .. 4g + 3; the nibbles of a
 //   dim in two tokens are interleaved into one byte, whose lookup in the
-//   value table gives (hi(t), hi(t')) and (lo(t), lo(t')), so the k-slots are
+//   value table gives (hi(t), lo(t)) and (hi(t'), lo(t')), so the k-slots are
 //   4 tokens x (hi, lo).  A = weights: row h holds the hi split of head h's
-//   weights, row 4 + h the lo split (moved there from lanes 0..3 by a
-//   row_shr:4 DPP move), in the k-slots of both the hi and lo value part.
+//   weights, row 4 + h the lo split, each weight as the pair (w, w) facing a
+//   token's (hi, lo) k-slots (gathered from the softmax lanes by DPP moves).
 //   One product covers 16 tokens x 16 dims; the output of head h is row h +
 //   row 4 + h (lane groups 0 and 1, one permlane16 swap at the end).
 //
@@ -80,7 +84,7 @@ struct Smem {
   static constexpr int kCurBytes = 2 * D * 4 + 2 * D;  // append mode: s_cur [2][D] + codes [2][D]
   static constexpr int kMisc = 1024;
   static constexpr int kStageBytes = 2 * 256 * 8;       // one copy of each table, staged before replication
-  static constexpr int kRedBytes = kWaves * 4 * D * 4;  // after the loop, inside the table area
+  static constexpr int kRedBytes = kWaves * 4 * (D + 10) * 4;  // after the loop, inside the table area
   static constexpr int kQb = 2 * kTableBytes;
   static constexpr int kQ = kQb + kQbBytes;
   static constexpr int kCur = kQ + kQBytes;
@@ -131,22 +135,16 @@ __device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, ui
   return __builtin_bit_cast(f16x8, u32x4{a, b, c, d});
 }
 
-__device__ __forceinline__ int table_shift(const float* __restrict__ cent) {
-  float mx = 0.f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(cent[j]));
-  return scale_shift(mx);
-}
-
 // Table entry e of one stream from its two centroids ce0 = c[e & 15],
-// ce1 = c[e >> 4]: (hi(ce0), hi(ce1)), (lo(ce0), lo(ce1)) of the centroids
-// scaled by 2^sh.
-__device__ __forceinline__ uint2 table_entry(float ce0, float ce1, int sh) {
+// ce1 = c[e >> 4], scaled by 2^sh: key table (hi(ce0), hi(ce1)),
+// (lo(ce0), lo(ce1)) (two dims of one token), value table (hi(ce0),
+// lo(ce0)), (hi(ce1), lo(ce1)) (one dim of two tokens).
+__device__ __forceinline__ uint2 table_entry(float ce0, float ce1, int sh, bool key) {
   const float c0 = ldexpf(ce0, sh), c1 = ldexpf(ce1, sh);
   const _Float16 h0 = static_cast<_Float16>(c0), h1 = static_cast<_Float16>(c1);
   const _Float16 l0 = static_cast<_Float16>(c0 - static_cast<float>(h0));
   const _Float16 l1 = static_cast<_Float16>(c1 - static_cast<float>(h1));
-  return make_uint2(pack_f16x2(h0, h1), pack_f16x2(l0, l1));
+  return key ? make_uint2(pack_f16x2(h0, h1), pack_f16x2(l0, l1)) : make_uint2(pack_f16x2(h0, l0), pack_f16x2(h1, l1));
 }
 
 // Replicates the staged entries (stage[t][e], t = 0 keys, 1 values) into the
@@ -196,24 +194,17 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   float* s_q = reinterpret_cast<float*>(smem + L::kQ);           // [4][D]
   float* s_cur = reinterpret_cast<float*>(smem + L::kCur);       // [2][D]
   uint8_t* s_codes = smem + L::kCur + 2 * D * 4;                 // [2][D]
-  float* s_misc = reinterpret_cast<float*>(smem + L::kMiscOff);  // [0..3] score scale per head, [4..7] shifts
+  float* s_misc = reinterpret_cast<float*>(smem + L::kMiscOff);  // [0..3] score scale per head, [4] output scale
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: row ranges and resources stay scalar
   const int n = lane & 15, g = lane >> 4;
 
-  // ---- work item (same XCD remap as decode_kernel: the splits of one head
-  // group share one XCD's L2).
-  const int units = a.num_layers * a.kv_heads * a.n_hgroups;
-  const int64_t nblk = static_cast<int64_t>(units) * a.n_splits;
-  int64_t gid = blockIdx.x;
-  if ((nblk & 7) == 0) gid = (gid & 7) * (nblk >> 3) + (gid >> 3);
-  const int unit = static_cast<int>(gid / a.n_splits);
-  const int split = static_cast<int>(gid - static_cast<int64_t>(unit) * a.n_splits);
-  const int lkv = unit / a.n_hgroups;
-  const int hg = unit - lkv * a.n_hgroups;
-  const int layer = lkv / a.kv_heads, kvh = lkv - layer * a.kv_heads;
-  const int qh0 = kvh * a.group + hg * 4;
+  // ---- work item: grid (split, head group, layer x KV head), so no
+  // division is needed; the query heads of (lkv, hg) start at lkv * group +
+  // 4 hg of the [L * Hq] rows.
+  const int split = blockIdx.x, hg = blockIdx.y, lkv = blockIdx.z;
+  const int64_t qhg0 = static_cast<int64_t>(lkv) * a.group + hg * 4;
 
   // Rows: blocks of kStride rows dealt out cyclically over the splits (split
   // s takes blocks s, s + n, s + 2n, ...), each block cut into
@@ -273,7 +264,9 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   // requested after the rows would wait for them.
   const float* cent_t = tid < 256 ? a.cent_k : a.cent_v;  // thread t stages entry t & 255 of table t / 256
   const float ce0 = cent_t[tid & 15], ce1 = cent_t[(tid >> 4) & 15];
-  const int sh_k = table_shift(a.cent_k), sh_v = table_shift(a.cent_v);
+  // power-of-two scale of this wavefront's table (key table for waves 0..3):
+  // the 16 lanes of a row hold all 16 centroids in ce0
+  const int sh_t = scale_shift(group_reduce<16, OpMax>(fabsf(ce0)));
   const bool appending = a.new_k != nullptr;
   const bool appender = appending && split == 0 && wave < 2;
   constexpr int kLevels = 15;
@@ -290,7 +283,7 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   }
   float qe[E], sg_first[E], sg_second[E];
   if (wave < 4) {
-    const int64_t qoff = (static_cast<int64_t>(layer) * a.query_heads + qh0 + wave) * D + lane * E;
+    const int64_t qoff = (qhg0 + wave) * D + lane * E;
 #pragma unroll
     for (int i = 0; i < E; ++i)
       qe[i] = QF16 ? __half2float(static_cast<const __half*>(a.q)[qoff + i]) : static_cast<const float*>(a.q)[qoff + i];
@@ -322,7 +315,8 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   };
 
   uint2* s_stage = reinterpret_cast<uint2*>(smem + L::kStage);  // [2][256]
-  s_stage[tid] = table_entry(ce0, ce1, tid < 256 ? sh_k : sh_v);
+  if (tid < 512) s_stage[tid] = table_entry(ce0, ce1, sh_t, tid < 256);  // stage[0][*] keys, stage[1][*] values
+  if (wave == 4 && lane == 0) s_misc[4] = ldexpf(1.f, -(sh_t + 7));  // weights carry 2^7, values 2^sh_v
 
   // ---- append mode: rotate (as on append) and quantize the new token.
   if (appender) {
@@ -357,7 +351,7 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
       s_qb[wave * L::kQbStride + lane * E + i] = __builtin_bit_cast(uint16_t, h);
       s_qb[(4 + wave) * L::kQbStride + lane * E + i] = __builtin_bit_cast(uint16_t, l);
     }
-    if (lane == 0) s_misc[wave] = ldexpf(1.f, -(sh_q + sh_k));  // raw score -> log2 units
+    if (lane == 0) s_misc[wave] = ldexpf(1.f, -(sh_q + sh_t));  // raw score -> log2 units
   }
   __syncthreads();
   replicate_tables(smem, s_stage, wave, lane);
@@ -378,23 +372,22 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   for (int i = 0; i < D / 8; ++i)
     qd[i] = n < 8 ? reinterpret_cast<const uint32_t*>(s_qb + n * L::kQbStride + g * (D / 4))[i] : 0u;
   const float score_scale = s_misc[n & 3];
-  const float out_scale = ldexpf(1.f, -(sh_v + 7));  // weights carry 2^7, values 2^sh_v
+  const float out_scale = s_misc[4];
 
   // table bases (offsets into smem): copy lane % 32, key table at 0, value
   // table at 65536; bits 8..15 stay clear for the code byte
   const uint32_t base_k = (lane & 31) * 8;
   const uint32_t base_v = base_k + kTableBytes;
 
-  // Softmax state, log2 units.  m_lane: running maximum of head n % 4
-  // (wavefront-wide: every lane sharing lane % 4 holds the same value).
-  // bias: 7 - m_lane on lanes n < 4 (the weights come out as p * 2^7, the
-  // scale of their exact f16 split), -inf elsewhere, so that the other lanes'
-  // weights are exp2(-inf) = 0 with no mask.  l_lane: this lane's softmax sum
-  // in units of 2^-7 (lanes n < 4).
-  const bool head_lane = n < 4;
+  // Softmax state, log2 units.  Lane m works on head m % 4: m_lane is that
+  // head's running maximum (wavefront-wide: every lane sharing m % 4 holds
+  // the same value); bias = 7 - m_lane (the weights come out as p * 2^7, the
+  // scale of their exact f16 split); l_lane is the lane's softmax sum in
+  // units of 2^-7.
   float m_lane = -INFINITY;
-  float bias = head_lane ? INFINITY : -INFINITY;  // +inf forces a maximum on the first tile
+  float bias = INFINITY;  // +inf forces a maximum on the first tile
   float l_lane = 0.f;
+  const int kk = (lane >> 2) & 3;  // this lane's token within its lane group's 4
   f32x4v acc[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) acc[j] = f32x4v{0.f, 0.f, 0.f, 0.f};
@@ -443,31 +436,36 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
       ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, ds, 0, 0, 0);
     }
   };
-  // Softmax and value products of tile k.  Lanes n < 4 hold head n's scores
-  // of tokens 4g + rr once column n + 4 (the query's lo split) is added; the
-  // other lanes' weights are zero through `bias`.  Only a split's last tiles
-  // can be partial: their rows past the end get weight zero.
+  // Softmax and value products of tile k.  After the score products lane
+  // (n, g) holds column n of tokens 4g + rr; column h + column h + 4 is head
+  // h's score (hi + lo query split, a row_ror:12 add), valid on lanes n < 4.
+  // The four registers are then spread over the row, so that lane m holds
+  // one score: head m % 4, token 4g + m / 4 % 4; the softmax runs once per
+  // lane, and the weights are gathered back into the A operand of the value
+  // products: row h (lanes n = h) the hi splits of head h's 4 tokens, row
+  // 4 + h their lo splits, each as an f16 pair (w, w) facing the value's
+  // (hi, lo) k-slots.  Rows 8..15 carry junk weights whose output rows are
+  // never read.  Only a split's last tiles can be partial.
   auto values = [&](const f32x4v& ds, int k) {
-    float sc[4], z[4];
+    float s4[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) s4[rr] = ds[rr] + dpp_move<kDppRor12>(ds[rr]);
+    float sc = s4[0];  // bank b (lanes 4b .. 4b + 3) takes register b from lanes 0..3
+    sc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, sc), __builtin_bit_cast(int, s4[1]),
+                                                               0x114, 0xf, 0x2, false));  // row_shr:4
+    sc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, sc), __builtin_bit_cast(int, s4[2]),
+                                                               0x118, 0xf, 0x4, false));  // row_shr:8
+    sc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, sc), __builtin_bit_cast(int, s4[3]),
+                                                               0x11C, 0xf, 0x8, false));  // row_shr:12
     const int row0 = tile_row(k);
     const bool full = row0 + kTile <= t1;  // wavefront-uniform
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      sc[rr] = ds[rr] + dpp_move<kDppRor12>(ds[rr]);  // column n + column n + 4
-      z[rr] = fmaf(sc[rr], score_scale, bias);
-    }
-    if (!full) {
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) z[rr] = row0 + 4 * g + rr < t1 ? z[rr] : -INFINITY;
-    }
-    const bool need = z[0] > kRescaleThreshold + kWeightExp || z[1] > kRescaleThreshold + kWeightExp ||
-                      z[2] > kRescaleThreshold + kWeightExp || z[3] > kRescaleThreshold + kWeightExp;
-    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+    const bool valid = full || row0 + 4 * g + kk < t1;
+    float z = fmaf(sc, score_scale, bias);
+    if (!full) z = valid ? z : -INFINITY;
+    if (__builtin_amdgcn_ballot_w64(z > kRescaleThreshold + kWeightExp) != 0) {
       // a running maximum moves: wavefront-wide per head (lanes sharing
-      // lane % 4), accumulators of head rr (rows rr, 4 + rr) rescaled
-      float mx = -INFINITY;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) mx = head_lane && row0 + 4 * g + rr < t1 ? fmaxf(mx, sc[rr] * score_scale) : mx;
+      // lane % 4); accumulators of head rr (rows rr, 4 + rr) rescaled
+      float mx = valid ? sc * score_scale : -INFINITY;
       mx = strided_reduce<4, OpMax>(mx);
       float alpha = 1.f;
       if (mx > m_lane + kRescaleThreshold) {
@@ -475,34 +473,29 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
         m_lane = mx;
       }
       l_lane *= alpha;
-      bias = head_lane ? kWeightExp - m_lane : -INFINITY;
+      bias = kWeightExp - m_lane;
       const f32x4v al = {quad_broadcast_t<0>(alpha), quad_broadcast_t<1>(alpha), quad_broadcast_t<2>(alpha),
                          quad_broadcast_t<3>(alpha)};
 #pragma unroll
       for (int j = 0; j < NV; ++j) acc[j] *= al;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) z[rr] = row0 + 4 * g + rr < t1 ? fmaf(sc[rr], score_scale, bias) : -INFINITY;
+      z = valid ? fmaf(sc, score_scale, bias) : -INFINITY;
     }
-    float p[4];
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      p[rr] = fast_exp2(z[rr]);  // p * 2^7
-      l_lane += p[rr];
-    }
+    const float p = fast_exp2(z);  // p * 2^7
+    l_lane += p;
     // exact split of p * 2^7: hi = low 13 mantissa bits cleared, lo = rest
-    uint32_t wh[2];
-#pragma unroll
-    for (int pr = 0; pr < 2; ++pr) {
-      const float x0 = p[2 * pr], x1 = p[2 * pr + 1];
-      const float h0 = __uint_as_float(__float_as_uint(x0) & 0xffffe000u);
-      const float h1 = __uint_as_float(__float_as_uint(x1) & 0xffffe000u);
-      wh[pr] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(h0, h1));
-      const uint32_t wl = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0 - h0, x1 - h1));
-      // rows 4..7 (lanes n = 4..7) take the lo split of head n - 4: row_shr:4, bank 1 only
-      wh[pr] = static_cast<uint32_t>(
-          __builtin_amdgcn_update_dpp(static_cast<int>(wh[pr]), static_cast<int>(wl), 0x114, 0xf, 0x2, false));
-    }
-    const f16x8 Aw = as_f16x8(wh[0], wh[0], wh[1], wh[1]);
+    const float ph = __uint_as_float(__float_as_uint(p) & 0xffffe000u);
+    const int whi = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pkrtz(ph, ph));
+    const int wlo = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pkrtz(p - ph, p - ph));
+    // gather: A register r holds token r of the lane group; lanes 0..3 read
+    // the hi pair of lane n + 4r, lanes 4..7 the lo pair of lane n - 4 + 4r
+    const int a0 = __builtin_amdgcn_update_dpp(whi, wlo, 0x114, 0xf, 0x2, false);  // row_shr:4 into lanes 4..7
+    int a1 = __builtin_amdgcn_update_dpp(wlo, whi, 0x104, 0xf, 0x1, false);         // row_shl:4 into lanes 0..3
+    int a2 = __builtin_amdgcn_update_dpp(whi, whi, 0x108, 0xf, 0x1, false);         // row_shl:8 into lanes 0..3
+    a2 = __builtin_amdgcn_update_dpp(a2, wlo, 0x104, 0xf, 0x2, false);              // row_shl:4 into lanes 4..7
+    int a3 = __builtin_amdgcn_update_dpp(whi, whi, 0x10C, 0xf, 0x1, false);         // row_shl:12 into lanes 0..3
+    a3 = __builtin_amdgcn_update_dpp(a3, wlo, 0x108, 0xf, 0x2, false);              // row_shl:8 into lanes 4..7
+    const f16x8 Aw = as_f16x8(static_cast<uint32_t>(a0), static_cast<uint32_t>(a1), static_cast<uint32_t>(a2),
+                              static_cast<uint32_t>(a3));
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const f16x8 B = as_f16x8(vl[j][0].x, vl[j][0].y, vl[j][1].x, vl[j][1].y);
@@ -538,21 +531,29 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   // ---- combine: rows h and 4 + h (lane groups 0 and 1), then the
   // wavefronts.  Lane n of group 0 holds head rr's output at dims of column n.
   __syncthreads();  // the tables are dead: reuse their space
-  float* s_red = reinterpret_cast<float*>(smem);                  // [kWaves][4][D]
-  float* s_mw = reinterpret_cast<float*>(smem + kWaves * 4 * D * 4);  // [kWaves][4]
-  float* s_lw = s_mw + kWaves * 4;                                 // [kWaves][4]
+  // s_red: [kWaves x 4 heads] rows of RS floats; dim d of a row sits at
+  // d + 4 (d / 64), and RS = D + 10, so that the 32 lanes writing one
+  // register pair (16 dims x 2 rows) hit 32 distinct banks
+  constexpr int RS = D + 10;
+  float* s_red = reinterpret_cast<float*>(smem);
+  float* s_mw = reinterpret_cast<float*>(smem + kWaves * 4 * RS * 4);  // [kWaves][4]
+  float* s_lw = s_mw + kWaves * 4;                                     // [kWaves][4]
+  auto red_pos = [](int d) { return d + 4 * (d >> 6); };
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    // dim of column n in product j: 8n + j (D = 128), 8n + j and 128 + 8n + j - 8 (D = 256), 4n + j (D = 64)
-    const int dim = D == 64 ? 4 * n + j : (j < 8 ? 8 * n + j : 128 + 8 * n + (j - 8));
+    // dim of column n in product j: 8n + j (D = 128), 4n + j (D = 64)
+    const int dim = D == 64 ? 4 * n + j : 8 * n + j;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const float v = xor_reduce<16, OpSum>(acc[j][rr]);
-      if (g == 0) s_red[(wave * 4 + rr) * D + dim] = v * out_scale;
+    for (int pr = 0; pr < 2; ++pr) {
+      // rows h (hi weights) and 4 + h (lo weights) of head h are lane groups
+      // 0 and 1; one permlane16 swap sums two registers: group 0 receives
+      // head 2pr's sum, group 1 head 2pr + 1's
+      const LanePair r = permlane_swap<16>(acc[j][2 * pr], acc[j][2 * pr + 1]);
+      if (g < 2) s_red[(wave * 4 + 2 * pr + g) * RS + red_pos(dim)] = r.first + r.second;
     }
   }
   {
-    const float lw = xor_reduce<32, OpSum>(xor_reduce<16, OpSum>(head_lane ? l_lane : 0.f)) * (1.f / 128.f);
+    const float lw = strided_reduce<4, OpSum>(l_lane) * (1.f / 128.f);  // head lane % 4
     if (lane < 4) {
       s_mw[wave * 4 + lane] = m_lane;
       s_lw[wave * 4 + lane] = lw;
@@ -568,7 +569,6 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
     for (int w = 0; w < kWaves; ++w) f[w] = s_mw[w * 4 + h] == -INFINITY ? 0.f : fast_exp2(s_mw[w * 4 + h] - M);
     return M;
   };
-  const int64_t qhg0 = static_cast<int64_t>(layer) * a.query_heads + qh0;
   if (wave < 4) {
     float f[kWaves];
     const float M = wave_weights(wave, f);
@@ -580,12 +580,12 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
     for (int i = 0; i < E; ++i) {
       float v = 0.f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) v = fmaf(s_red[(w * 4 + wave) * D + lane * E + i], f[w], v);
-      e[i] = v;
+      for (int w = 0; w < kWaves; ++w) v = fmaf(s_red[(w * 4 + wave) * RS + red_pos(lane * E + i)], f[w], v);
+      e[i] = v * out_scale;
     }
     if (a.n_splits == 1) {
       // one split: finish the row here (current token, normalisation, inverse rotation)
-      float* row = s_red + wave * D;  // wavefront `wave` owns this row of the first block now
+      float* row = s_red + wave * RS;  // row (wave 0, head `wave`): read only by this wavefront
 #pragma unroll
       for (int i = 0; i < E; ++i) row[lane * E + i] = e[i];
       const float* ck = appending ? s_cur : a.cur_k ? a.cur_k + static_cast<int64_t>(lkv) * D : nullptr;

@@ -1404,28 +1404,34 @@ int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hi
 int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream);
 
 template <int D, bool QF16>
-void launch_mx_t(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+void launch_mx_t(const DecodeArgs& a, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (start != nullptr || stop != nullptr)
-    hipExtLaunchKernelGGL((decode_mx_kernel<D, QF16>), dim3(nblk), dim3(mx::kThreads), 0, stream, start, stop, 0, a);
+    hipExtLaunchKernelGGL((decode_mx_kernel<D, QF16>), grid, dim3(mx::kThreads), 0, stream, start, stop, 0, a);
   else
-    hipLaunchKernelGGL((decode_mx_kernel<D, QF16>), dim3(nblk), dim3(mx::kThreads), 0, stream, a);
+    hipLaunchKernelGGL((decode_mx_kernel<D, QF16>), grid, dim3(mx::kThreads), 0, stream, a);
 }
 
 template <int D>
-void launch_mx_d(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+void launch_mx_d(const DecodeArgs& a, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (a.q_f16)
-    launch_mx_t<D, true>(a, nblk, stream, start, stop);
+    launch_mx_t<D, true>(a, grid, stream, start, stop);
   else
-    launch_mx_t<D, false>(a, nblk, stream, start, stop);
+    launch_mx_t<D, false>(a, grid, stream, start, stop);
 }
 
-int launch_mx(const DecodeArgs& a, int head_dim, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+// Grid (split, head group, layer x KV head) of decode_mx_kernel.
+int launch_mx(const DecodeArgs& a, int head_dim, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  constexpr int kMaxGridYZ = 65535;
+  const int lkv = a.num_layers * a.kv_heads;
+  if (lkv > kMaxGridYZ || a.n_hgroups > kMaxGridYZ)
+    return fail(TQ_ERR_BAD_ARG, "num_layers x kv_heads must be at most 65535 per call; decode fewer layers per call");
+  const dim3 grid(a.n_splits, a.n_hgroups, lkv);
   switch (head_dim) {
     case 64:
-      launch_mx_d<64>(a, nblk, stream, start, stop);
+      launch_mx_d<64>(a, grid, stream, start, stop);
       return TQ_OK;
     case 128:
-      launch_mx_d<128>(a, nblk, stream, start, stop);
+      launch_mx_d<128>(a, grid, stream, start, stop);
       return TQ_OK;
     default:
       return fail(TQ_ERR_UNSUPPORTED, "decode_mx_kernel: unsupported head dimension " + std::to_string(head_dim));
@@ -1540,7 +1546,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   m.out = out;
 
   if (p.kernel == SplitKernel::Mx) {
-    rc = launch_mx(a, head_dim, nblk, stream, start, stop);
+    rc = launch_mx(a, head_dim, stream, start, stop);
   } else {
     rc = launch_fp32(a, fmt, head_dim, p.hg, nblk, stream, start, stop);
   }
