@@ -110,44 +110,126 @@ def synthetic(seed, layers, kv_heads, query_heads, seq_len, head_dim, std):
     return q.astype(np.float16), k.astype(np.float16), v.astype(np.float16)
 
 
-def cpu_baseline(q, k_codes, v_codes, cache, head_subset: int, budget_s: float, gpu_out, k_scales=None, v_scales=None):
-    """Time the CPU oracle (vectorised numpy restatement of cache.py:98-140) on a bounded sample.
+_CPU_JOB: dict = {}
 
-    Sample: the first `head_subset` KV heads (and their query heads) at the full
-    sequence length, repeated until `budget_s` seconds have elapsed; the time
-    is scaled to the full head count.  Single-threaded numpy.
+
+def _cpu_head(qh: int):
+    """Worker: the oracle decode of query head qh against its KV head (cache.py:98-140 restated, which
+    expands the KV rows per query head), single-threaded."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import torque_oracle as o
+
+    j = _CPU_JOB
+    h = qh // j["group"]
+    with threadpool_limits(1):
+        q_rot = o.rotation_apply(j["q"][:, qh : qh + 1], j["sl"], j["sr"])[0]
+        idx = np.array([h])
+        out_rot = o.decode_packed_reference(
+            q_rot, j["kc"][0][idx], j["vc"][0][idx], j["kcent"], j["vcent"], bit_width=j["bits"],
+            head_dim=j["head_dim"], key_scales=None if j["ks"] is None else j["ks"][0][idx],
+            value_scales=None if j["vs"] is None else j["vs"][0][idx],
+        )
+        return qh, o.rotation_inverse(out_rot, j["sl"], j["sr"])[0]
+
+
+def cpu_pool_size() -> int:
+    """Worker processes for the CPU baseline: every core this process may run on, at most 16 (one GPU's
+    share of the box's host cores)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def cpu_baseline(q, k_codes, v_codes, cache, budget_s: float, gpu_out, k_scales=None, v_scales=None):
+    """Time the CPU oracle (vectorised numpy restatement of cache.py:98-140) on all host cores.
+
+    One step decodes every query head at the full sequence length, one query
+    head per task on a pool of forked single-threaded workers; steps repeat
+    until `budget_s` seconds have elapsed and the median step is reported.
     """
+    import multiprocessing as mp
+    from concurrent.futures import ProcessPoolExecutor
+
+    cfg = cache.config
+    _CPU_JOB.update(
+        group=q.shape[1] // cfg.kv_heads, q=q.astype(np.float32), kc=k_codes, vc=v_codes, ks=k_scales, vs=v_scales,
+        sl=cache.rotation.signs_left, sr=cache.rotation.signs_right, kcent=cache.key_codebook.centroids,
+        vcent=cache.value_codebook.centroids, bits=cfg.bit_width, head_dim=cfg.head_dim,
+    )
+    workers = cpu_pool_size()
+    hq = q.shape[1]
+    out = np.zeros((hq, cfg.head_dim), np.float32)
+    times = []
+    with ProcessPoolExecutor(max_workers=workers, mp_context=mp.get_context("fork")) as pool:
+        list(pool.map(_cpu_head, range(min(workers, hq))))  # fork and warm the workers
+        t_start = time.perf_counter()
+        while time.perf_counter() - t_start < budget_s or len(times) < 1:
+            t0 = time.perf_counter()
+            for qh, o_h in pool.map(_cpu_head, range(hq)):
+                out[qh] = o_h
+            times.append(time.perf_counter() - t0)
+    _CPU_JOB.clear()
+    per_step = float(np.median(times))
+    ref = gpu_out[0]
+    err = float(np.max(np.abs(ref - out)))
+    rel = float(np.linalg.norm(ref - out) / max(np.linalg.norm(out), 1e-30))
+    return per_step, len(times), workers, err, rel
+
+
+def cpu_literal_baseline(q, k_codes, v_codes, cache, budget_s: float):
+    """The reference's literal per-element path, timed single-threaded: the per-code unpack loop of
+    quantization.py:272-290 for every row, centroid gather, then the online-softmax loop of
+    reference.py:8-42 token by token for every query head (the oracle's unpack_indices and
+    streaming_attention_decode), with the rotations of cache.py:98-140.  Small workloads only."""
     from oracle import torque_oracle as o
 
     cfg = cache.config
     g = q.shape[1] // cfg.kv_heads
-    qs = q[:, : head_subset * g].astype(np.float32)
-    kc, vc = k_codes[:, :head_subset], v_codes[:, :head_subset]
-    ks = None if k_scales is None else k_scales[:, :head_subset]
-    vs = None if v_scales is None else v_scales[:, :head_subset]
     sl, sr = cache.rotation.signs_left, cache.rotation.signs_right
     kcent, vcent = cache.key_codebook.centroids, cache.value_codebook.centroids
 
     def one():
-        q_rot = o.rotation_apply(qs, sl, sr)[0]
-        idx = np.arange(q_rot.shape[0]) // g
-        out_rot = o.decode_packed_reference(
-            q_rot, kc[0][idx], vc[0][idx], kcent, vcent, bit_width=cfg.bit_width, head_dim=cfg.head_dim,
-            key_scales=None if ks is None else ks[0][idx], value_scales=None if vs is None else vs[0][idx],
-        )
-        return o.rotation_inverse(out_rot, sl, sr)
+        q_rot = o.rotation_apply(q.astype(np.float32), sl, sr)[0]
+        out = np.empty_like(q_rot)
+        for h in range(cfg.kv_heads):
+            keys = o.dequantize(np.stack([o.unpack_indices(w, cfg.bit_width, cfg.head_dim) for w in k_codes[0, h]]), kcent)
+            values = o.dequantize(np.stack([o.unpack_indices(w, cfg.bit_width, cfg.head_dim) for w in v_codes[0, h]]), vcent)
+            for j in range(g):
+                out[h * g + j] = o.streaming_attention_decode(q_rot[h * g + j], keys, values)
+        return o.rotation_inverse(out, sl, sr)
 
-    times, out = [], None
+    times = []
     t_start = time.perf_counter()
     while time.perf_counter() - t_start < budget_s or len(times) < 1:
         t0 = time.perf_counter()
-        out = one()
+        one()
         times.append(time.perf_counter() - t0)
-    per_step = float(np.median(times)) * cfg.kv_heads / head_subset
-    ref = gpu_out[0, : head_subset * g]
-    err = float(np.max(np.abs(ref - out)))
-    rel = float(np.linalg.norm(ref - out) / max(np.linalg.norm(out), 1e-30))
-    return per_step, len(times), err, rel
+    return float(np.median(times)), len(times)
+
+
+FP16_MATRIX_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
+
+
+def compute_roofline(matrix_kernel: bool, L: int, hkv: int, hq: int, d: int, s: int, kern_us: float) -> dict:
+    """The split kernel against its arithmetic ceiling.
+
+    Algorithmic work: 4 L Hq S D flops per step (a multiply-add per query head
+    and packed code for the score and for the value update).  The float32
+    kernel runs it as 4x4x1 fp32 products (fp32 matrix peak); the matrix
+    kernel as 16x16x32 f16 products of hi/lo splits (fp16 matrix peak), which
+    execute 16 products of 16x16x32 per 16-token tile and group of 4 query
+    heads (half of each product's rows or columns carry data).
+    """
+    algo = 4 * L * hq * s * d
+    if matrix_kernel:
+        tiles = L * hkv * (hq // hkv // 4) * ((s + 15) // 16)
+        executed = tiles * (d // 16) * 2 * 2 * 16 * 16 * 32
+        tflops = executed / (kern_us * 1e-6) / 1e12
+        return {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP16_MATRIX_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / FP16_MATRIX_PEAK_TFLOPS, 4), "flops_per_launch": executed,
+                "algorithmic_flops_per_launch": algo}
+    tflops = algo / (kern_us * 1e-6) / 1e12
+    return {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MATRIX_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / FP32_MATRIX_PEAK_TFLOPS, 4), "flops_per_launch": algo}
 
 
 def measured_traffic(kernel: str, workload: str) -> tuple[int | None, str | None]:
@@ -352,6 +434,11 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "arithmetic": (
+            "float32 accumulation of exact float16 hi/lo split products (16x16x32 matrix cores); "
+            "softmax, merge and rotations in float32" if matrix_kernel else
+            "float32 products and accumulation (4x4x1 fp32 matrix products / VALU FMAs)"
+        ),
         "data": "synthetic",
         "config": {
             "workload": desc,
@@ -483,7 +570,8 @@ def main() -> int:
         torch.randn((L, hq, d), generator=torch.Generator(device=dev).manual_seed(i), device=dev).half()
         for i in range(1, 4)
     ]
-    n_splits = args.splits or ops.plan_splits(L, hkv, hq, d, s, dev, bit_width=bits)
+    n_splits = args.splits or ops.plan_splits(L, hkv, hq, d, s, dev, bit_width=bits,
+                                              flags=_lib.TQ_F32_PRODUCTS if scaled else 0)
     ws = ops.workspace_for(L, hkv, hq, d, n_splits, dev)
     out = torch.empty((L, hq, d), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
@@ -533,9 +621,39 @@ def main() -> int:
     kern_us = float(np.mean(kern_ms) * 1e3)
     kern_med_us = float(np.median(kern_ms) * 1e3)
     achieved = algo_bytes / (kern_us * 1e-6) / 1e9
-    kernel_name = f"decode_kernel<PackedB{bits},{d},4{',scaled' if scaled else ''}>"
+    kernel_name = _lib.split_kernel(hkv, hq, d, bits, flags | (_lib.TQ_F32_PRODUCTS if scaled else 0), _lib.TQ_F16)
+    matrix_kernel = kernel_name.startswith("decode_mx_kernel")
+    if scaled:
+        kernel_name += ",scaled"
     traffic, traffic_src = measured_traffic(kernel_name, args.workload)
-    log(f"decode kernel mean {kern_us:.2f} us (median {kern_med_us:.2f}), wall {ms_per_step * 1e3:.2f} us/step")
+    log(f"decode kernel {kernel_name}: mean {kern_us:.2f} us (median {kern_med_us:.2f}), "
+        f"wall {ms_per_step * 1e3:.2f} us/step")
+
+    f32_products = None
+    if matrix_kernel:
+        # the float32-product split kernel on the same calls (TQ_F32_PRODUCTS), timed the same way
+        # call tuple (unscaled): ..., signs_right, flags [15], cur_k, cur_v, n_splits [18], ws, ws bytes, out, stream
+        n_f32 = ops.plan_splits(L, hkv, hq, d, s, dev, bit_width=bits, flags=flags | _lib.TQ_F32_PRODUCTS)
+        ws32 = ops.workspace_for(L, hkv, hq, d, n_f32, dev)
+        f32_args = [a[:15] + (flags | _lib.TQ_F32_PRODUCTS, None, None, n_f32, ws32.data_ptr(), ws32.numel()) + a[21:]
+                    for a in call_args]
+        for i in range(args.warmup):
+            _lib.check(fn(*f32_args[i % n_rep], None, None))
+        evs32 = [(hip.event(), hip.event()) for _ in range(n_ev)]
+        torch.cuda.synchronize()
+        for i in range(n_ev):
+            _lib.check(fn(*f32_args[i % n_rep], evs32[i][0], evs32[i][1]))
+        torch.cuda.synchronize()
+        k32 = np.array([hip.elapsed_ms(a, b) for a, b in evs32]) * 1e3
+        f32_products = {
+            "kernel": _lib.split_kernel(hkv, hq, d, bits, flags | _lib.TQ_F32_PRODUCTS, _lib.TQ_F16),
+            "n_splits": n_f32,
+            "kernel_us_per_step": round(float(np.mean(k32)), 3),
+            "kernel_us_median": round(float(np.median(k32)), 3),
+            "frac": round(algo_bytes / (float(np.mean(k32)) * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        }
+        log(f"float32-product kernel {f32_products['kernel']}: mean {f32_products['kernel_us_per_step']:.2f} us "
+            f"(median {f32_products['kernel_us_median']:.2f})")
 
     result = {
         "metric": METRIC,
@@ -549,6 +667,11 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "arithmetic": (
+            "float32 accumulation of exact float16 hi/lo split products (16x16x32 matrix cores); "
+            "softmax, merge and rotations in float32" if matrix_kernel else
+            "float32 products and accumulation (4x4x1 fp32 matrix products / VALU FMAs)"
+        ),
         "data": "synthetic",
         "config": {
             "workload": desc,
@@ -577,19 +700,10 @@ def main() -> int:
             "kernel": kernel_name,
             "algorithmic_bytes_per_launch": algo_bytes,
         },
-        # The same kernel against its arithmetic ceiling: 4 L Hq S D flops per
-        # step (a multiply-add per query head and packed code for the score
-        # and for the value update), fp32, which the split kernel runs as
-        # 4x4x1 fp32 products on the matrix cores for groups of 4 query heads.
-        "roofline_compute": {
-            "bound": "mfma",
-            "achieved": round(4 * L * hq * s * d / (kern_us * 1e-6) / 1e12, 2),
-            "peak": FP32_MATRIX_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(4 * L * hq * s * d / (kern_us * 1e-6) / 1e12 / FP32_MATRIX_PEAK_TFLOPS, 4),
-            "flops_per_launch": 4 * L * hq * s * d,
-        },
+        "roofline_compute": compute_roofline(matrix_kernel, L, hkv, hq, d, s, kern_us),
     }
+    if f32_products is not None:
+        result["f32_products"] = f32_products
 
     if not args.no_dense:
         # fp16-dense comparator: same shape, dense K/V fp16 slabs, same split-K kernel structure
@@ -631,21 +745,36 @@ def main() -> int:
     if not args.no_cpu_baseline:
         kc_np = store.key_codes[:, :, :s].cpu().numpy().view(np.uint32)
         vc_np = store.value_codes[:, :, :s].cpu().numpy().view(np.uint32)
-        subset = 1 if s * d > 2**23 else hkv
         ks_np = store.key_scales[:, :, :s].cpu().numpy() if scaled else None
         vs_np = store.value_scales[:, :, :s].cpu().numpy() if scaled else None
-        per_step, n, err, rel = cpu_baseline(q_np, kc_np, vc_np, cache, subset, args.cpu_budget, gpu_out0, ks_np, vs_np)
+        per_step, n, workers, err, rel = cpu_baseline(q_np, kc_np, vc_np, cache, args.cpu_budget, gpu_out0, ks_np, vs_np)
         result["cpu_baseline"] = {
             "value": round(packed_bytes / per_step / 1e9, 4),
             "unit": "GB/s",
             "us_per_step": round(per_step * 1e6, 1),
-            "cores": 1,
+            "cores": workers,
             "kind": "port",
-            "sample": f"numpy oracle decode of KV heads 0..{subset - 1} (of {hkv}) with their query heads at the full "
-            f"sequence length, {n} repetitions, median scaled by {hkv}/{subset}",
+            "sample": f"numpy oracle decode of all {hq} query heads at the full sequence length, one query head "
+            f"per task on {workers} forked single-threaded worker processes, {n} steps, median",
+            "host_cpu_count": os.cpu_count(),
+            "host_affinity_cores": len(os.sched_getaffinity(0)),
+            "thread_env": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")},
+            "worker_threads": 1,
         }
-        result["parity_vs_oracle"] = {"max_abs": err, "rel_l2": rel, "heads_checked": subset * (hq // hkv)}
-        log(f"cpu baseline {per_step * 1e6:.0f} us/step; parity max-abs {err:.2e} rel-L2 {rel:.2e}")
+        result["parity_vs_oracle"] = {"max_abs": err, "rel_l2": rel, "heads_checked": hq}
+        log(f"cpu baseline {per_step * 1e6:.0f} us/step on {workers} processes; parity max-abs {err:.2e} rel-L2 {rel:.2e}")
+        if L * hkv * s <= 8 * 1024 and not scaled:
+            lit, n_lit = cpu_literal_baseline(q_np, kc_np, vc_np, cache, min(args.cpu_budget, 10.0))
+            result["cpu_baseline_literal"] = {
+                "value": round(packed_bytes / lit / 1e9, 6),
+                "unit": "GB/s",
+                "us_per_step": round(lit * 1e6, 1),
+                "cores": 1,
+                "kind": "port",
+                "sample": "literal per-element path, single thread: per-code unpack loop (quantization.py:272-290) "
+                f"of every row and the per-token online-softmax loop (reference.py:8-42), {n_lit} steps, median",
+            }
+            log(f"cpu literal per-element path {lit * 1e6:.0f} us/step")
 
     if args.calibration_copy_mib > 0:
         n = args.calibration_copy_mib * 2**20 // 4

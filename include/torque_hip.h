@@ -126,6 +126,14 @@ int tq_unpack_dequantize_scaled(const uint32_t* codes, const float* scales, int6
 int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int head_dim, int bits, int flags,
                              int64_t seq_len, int num_cus);
 
+/* Name of the split kernel a tq_decode call over `bits`-bit packed rows with
+ * decode `flags` and a query of `query_dtype` launches:
+ * "decode_mx_kernel<D,QF16>" (the float16-split matrix kernel) or
+ * "decode_kernel<PackedB<bits>,D,<heads per group>>" (the float32 kernel;
+ * tq_decode_scaled always runs this one).  For profiles and benchmarks; no
+ * reference counterpart.  NULL on bad arguments (tq_last_error). */
+const char* tq_decode_split_kernel(int kv_heads, int query_heads, int head_dim, int bits, int flags, int query_dtype);
+
 /* Bytes of workspace tq_decode / tq_decode_dense need for n_splits splits
  * (n_splits <= 0: enough for the default split count on any sequence length
  * with num_cus compute units).  The workspace holds per-split partial results

@@ -46,7 +46,7 @@ def test_host_only_entry_points():
 
     lib = _lib.load()
     assert lib.tq_abi_version() == _lib.ABI_VERSION == 2
-    # 4-bit rows in groups of 4 query heads: the f16-split matrix kernel, one 512-thread workgroup per CU
+    # 4-bit rows in groups of 4 query heads: the f16-split matrix kernel, one 768-thread workgroup per CU
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 32768, 256) == 32
     # the float32-product kernel (requested, or 2-bit rows): two 256-thread workgroups per CU
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 4, 32768, 256) == 64
@@ -54,6 +54,14 @@ def test_host_only_entry_points():
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 7, 256) == 1
     assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, 64, 256) > 64 * 8 * 4 * 128 * 4
     assert lib.tq_decode_workspace_bytes(1, 8, 30, 128, 64, 256) == 0  # Hq not divisible
+    assert _lib.split_kernel(8, 32, 128, 4, 0, _lib.TQ_F16) == "decode_mx_kernel<128,true>"
+    assert _lib.split_kernel(8, 32, 64, 4, 0, _lib.TQ_F32) == "decode_mx_kernel<64,false>"
+    assert _lib.split_kernel(8, 32, 128, 4, _lib.TQ_F32_PRODUCTS, _lib.TQ_F16) == "decode_kernel<PackedB4,128,4>"
+    assert _lib.split_kernel(8, 32, 128, 2, 0, _lib.TQ_F16) == "decode_kernel<PackedB2,128,4>"
+    assert _lib.split_kernel(2, 8, 256, 4, 0, _lib.TQ_F16) == "decode_kernel<PackedB4,256,4>"
+    assert _lib.split_kernel(4, 8, 128, 4, 0, _lib.TQ_F16) == "decode_kernel<PackedB4,128,2>"
+    with pytest.raises(ValueError):
+        _lib.split_kernel(8, 30, 128, 4, 0, _lib.TQ_F16)
 
 
 @pytest.mark.parametrize(

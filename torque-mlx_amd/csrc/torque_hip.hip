@@ -1193,7 +1193,7 @@ int pick_hg(int group) {
 // The split kernel a decode call runs: the float32 kernel (decode_kernel,
 // 4x4x1 fp32 matrix products or VALU FMAs, 256 threads, two workgroups per
 // CU) or, for 4-bit packed rows in groups of 4 query heads at head_dim 64 or
-// 128, decode_mx_kernel (16x16x32 products of exact f16 splits, 512 threads,
+// 128, decode_mx_kernel (16x16x32 products of exact f16 splits, 768 threads,
 // one workgroup per CU) unless TQ_F32_PRODUCTS asks for the former.
 enum class SplitKernel { Fp32, Mx };
 
@@ -2020,6 +2020,27 @@ int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int 
   const int units = num_layers * kv_heads * (group / hg);
   const bool mx_kernel = pick_kernel(bits, head_dim, hg, flags) == SplitKernel::Mx;
   return default_splits(units, seq_len, num_cus, mx_kernel ? 1 : 2);
+}
+
+const char* tq_decode_split_kernel(int kv_heads, int query_heads, int head_dim, int bits, int flags,
+                                   int query_dtype) {
+  if (kv_heads <= 0 || query_heads <= 0 || query_heads % kv_heads != 0 || !valid_head_dim(head_dim)) {
+    fail(TQ_ERR_BAD_ARG, "bad head configuration");
+    return nullptr;
+  }
+  const bool packed = bits == 2 || bits == 3 || bits == 4;
+  if (!packed) {
+    fail(TQ_ERR_UNSUPPORTED, "split kernel names cover packed rows (bits 2, 3, 4)");
+    return nullptr;
+  }
+  const int hg = pick_hg(query_heads / kv_heads);
+  static thread_local std::string name;
+  if (pick_kernel(bits, head_dim, hg, flags) == SplitKernel::Mx)
+    name = "decode_mx_kernel<" + std::to_string(head_dim) + "," + (query_dtype == TQ_F16 ? "true" : "false") + ">";
+  else
+    name = "decode_kernel<PackedB" + std::to_string(bits) + "," + std::to_string(head_dim) + "," +
+           std::to_string(hg) + ">";
+  return name.c_str();
 }
 
 size_t tq_decode_workspace_bytes(int num_layers, int kv_heads, int query_heads, int head_dim, int n_splits,

@@ -54,6 +54,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tq_unpack_dequantize": (_i, [_p, _i64, _i64, _i64, _i, _i, _p, _p, _p]),
     "tq_unpack_dequantize_scaled": (_i, [_p, _p, _i64, _i64, _i64, _i, _i, _p, _p, _p]),
     "tq_decode_default_splits": (_i, [_i, _i, _i, _i, _i, _i, _i64, _i]),
+    "tq_decode_split_kernel": (ctypes.c_char_p, [_i, _i, _i, _i, _i, _i]),
     "tq_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "tq_decode": (
         _i,
@@ -136,7 +137,7 @@ def check(rc: int) -> None:
     raise TorqueHIPError(message or f"libtorque_hip error {rc}")
 
 
-_NOT_STATUS = {"tq_abi_version", "tq_last_error", "tq_decode_workspace_bytes"}
+_NOT_STATUS = {"tq_abi_version", "tq_last_error", "tq_decode_workspace_bytes", "tq_decode_split_kernel"}
 
 
 def call(name: str, *args) -> int:
@@ -146,6 +147,14 @@ def call(name: str, *args) -> int:
     if name not in _NOT_STATUS and rc < 0:
         check(rc)
     return rc
+
+
+def split_kernel(kv_heads: int, query_heads: int, head_dim: int, bits: int, flags: int, query_dtype: int) -> str:
+    """Name of the split kernel tq_decode launches for this shape and flags (tq_decode_split_kernel)."""
+    name = load().tq_decode_split_kernel(kv_heads, query_heads, head_dim, bits, flags, query_dtype)
+    if name is None:
+        raise ValueError(load().tq_last_error().decode("utf-8", "replace"))
+    return name.decode()
 
 
 def hip_available() -> bool:
