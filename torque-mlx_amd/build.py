@@ -1,6 +1,7 @@
 """Build recipe for libtorque_hip.so (gfx950).
 
     python torque-mlx_amd/build.py            # or __graft_entry__.build()
+    python torque-mlx_amd/build.py --asan OUT.so   # host-only AddressSanitizer build
 
 Compiles csrc/torque_hip.hip with hipcc into torque_hip/libtorque_hip.so,
 in-tree.  Packed-FP32 VALU ops are disabled for all device code.  The
@@ -46,8 +47,27 @@ def hipcc() -> str:
     return path
 
 
-def build_library(verbose: bool = False) -> Path:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(REPO / "include"), "-I", str(ROOT / "csrc"), str(SOURCE), "-o", str(OUTPUT) + ".tmp"]
+# Host-only AddressSanitizer build (argument validation, split planning,
+# workspace checks): the host pass is instrumented, the gfx950 code is not.
+ASAN_FLAGS = ["-O1", "-g", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer", "-shared-libasan"]
+
+
+def asan_runtime() -> Path:
+    """The clang AddressSanitizer runtime a process must preload to load the ASan build."""
+    hits = sorted(Path(hipcc()).resolve().parents[1].glob("lib/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not hits:
+        raise RuntimeError("libclang_rt.asan-x86_64.so not found next to hipcc")
+    return hits[-1]
+
+
+def build_library(verbose: bool = False, asan: bool = False, output: Path | None = None) -> Path:
+    """Compile the library to `output` (default: the in-tree libtorque_hip.so; the ASan build has no
+    default location and needs one)."""
+    if asan and output is None:
+        raise ValueError("the AddressSanitizer build needs an output path outside the package")
+    out = Path(output) if output is not None else OUTPUT
+    flags = [f for f in HIPCC_FLAGS if not (asan and f == "-O3")] + (ASAN_FLAGS if asan else [])
+    cmd = [hipcc(), *flags, "-I", str(REPO / "include"), "-I", str(ROOT / "csrc"), str(SOURCE), "-o", str(out) + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -55,11 +75,14 @@ def build_library(verbose: bool = False) -> Path:
     stderr = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{stderr}")
-    os.replace(str(OUTPUT) + ".tmp", OUTPUT)
+    os.replace(str(out) + ".tmp", out)
     if verbose and stderr.strip():
         print(stderr, file=sys.stderr)
-    return OUTPUT
+    return out
 
 
 if __name__ == "__main__":
-    print(build_library(verbose=True))
+    if "--asan" in sys.argv:
+        print(build_library(verbose=True, asan=True, output=Path(sys.argv[sys.argv.index("--asan") + 1])))
+    else:
+        print(build_library(verbose=True))
