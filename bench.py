@@ -305,6 +305,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
 
     stores = [c._store for c in caches]
     w = stores[0].layout.packed_words
+    matrix_kernel = _lib.split_kernel(hkv, hq, d, bits, 0, _lib.TQ_F16).startswith("decode_mx_kernel")
     n_splits = [ops.plan_splits(1, hkv, hq, d, s0 + steps, dev, bit_width=bits) for _ in range(L)]
     ws = ops.workspace_for(1, hkv, hq, d, args.splits, dev)
     out = torch.empty((L, hq, d), dtype=torch.float32, device=dev)
@@ -343,7 +344,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
             _lib.check(lib.tq_decode(queries[0, l].data_ptr(), _lib.TQ_F16, 1, hq, hkv, d, bits, st.key_codes.data_ptr(),
                                      st.value_codes.data_ptr(), st.capacity, s0, st.key_centroids.data_ptr(),
                                      st.value_centroids.data_ptr(), st.signs_left.data_ptr(),
-                                     st.signs_right.data_ptr(), dflags, None, None, 0, ws.data_ptr(), ws.numel(),
+                                     st.signs_right.data_ptr(), dflags, None, None, args.splits, ws.data_ptr(), ws.numel(),
                                      out[l].data_ptr(), stream))
     # a 1 GiB read between steps evicts the slabs from the 256 MB Infinity Cache; it is outside the events
     flush = torch.empty(2**30, dtype=torch.uint8, device=dev)
