@@ -608,6 +608,7 @@ def main() -> int:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     run(args.steps)
+    t_enq = time.perf_counter() - t0
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
@@ -628,7 +629,7 @@ def main() -> int:
         kernel_name += ",scaled"
     traffic, traffic_src = measured_traffic(kernel_name, args.workload)
     log(f"decode kernel {kernel_name}: mean {kern_us:.2f} us (median {kern_med_us:.2f}), "
-        f"wall {ms_per_step * 1e3:.2f} us/step")
+        f"wall {ms_per_step * 1e3:.2f} us/step (host enqueue {t_enq * 1e6 / args.steps:.2f} us/step)")
 
     f32_products = None
     if matrix_kernel:
@@ -689,6 +690,7 @@ def main() -> int:
         },
         "kernel_us_per_step": round(kern_us, 3),
         "kernel_us_median": round(kern_med_us, 3),
+        "host_enqueue_us_per_step": round(t_enq * 1e6 / args.steps, 2),
         "pct_peak": round(100.0 * achieved / HBM_PEAK_GBPS, 2),
         "roofline": {
             "bound": "hbm",

@@ -282,6 +282,44 @@ def test_strategies(hip_device):
         np.testing.assert_allclose(out, exp, atol=2e-5, rtol=1e-4, err_msg=s)
 
 
+@pytest.mark.parametrize("prefill", [0, 1, 700])
+def test_profiled_decode_with_current_and_decode_append(hip_device, prefill):
+    """profile_decode_components on decode_with_current and decode_append runs the reference's staged
+    path with the current token (cache_mlx.py:565-640) and records its stage keys, including
+    tail_seconds; outputs (and, for decode_append, packed words and length) equal the unprofiled calls."""
+    import torque_hip as th
+
+    rng = np.random.default_rng(prefill + 3)
+    cfg = th.TorqueConfig(bit_width=4, head_dim=128, num_layers=2, kv_heads=2)
+    kw = dict(config=cfg, key_codebook=th.build_gaussian_codebook(4, seed=0),
+              value_codebook=th.build_gaussian_codebook(4, seed=1), initial_capacity=8)
+    plain, profiled = th.TorqueKVCacheHIP(**kw), th.TorqueKVCacheHIP(**kw, profile_decode_components=True)
+    if prefill:
+        k0 = rng.normal(size=(2, 2, prefill, 128)).astype(np.float32)
+        v0 = rng.normal(size=(2, 2, prefill, 128)).astype(np.float32)
+        plain.append_many(key=k0, value=v0)
+        profiled.append_many(key=k0, value=v0)
+    stage_keys = {"packed_score_seconds", "softmax_seconds", "packed_value_seconds", "tail_seconds"}
+    for step in range(3):
+        q = rng.normal(size=(2, 8, 128)).astype(np.float32)
+        k = rng.normal(size=(2, 2, 128)).astype(np.float32)
+        v = rng.normal(size=(2, 2, 128)).astype(np.float32)
+        exp = plain.decode_with_current(query=q, key=k, value=v)
+        got = profiled.decode_with_current(query=q, key=k, value=v)
+        np.testing.assert_allclose(got, exp, atol=2e-6, rtol=1e-5, err_msg=f"with_current step {step}")
+        keys = set(profiled.last_decode_profile)
+        assert (stage_keys if plain.sequence_length else {"tail_seconds"}) <= keys, keys
+        exp = plain.decode_append(query=q, key=k, value=v)
+        got = profiled.decode_append(query=q, key=k, value=v)
+        np.testing.assert_allclose(got, exp, atol=2e-6, rtol=1e-5, err_msg=f"decode_append step {step}")
+        assert "append_seconds" in profiled.last_decode_profile
+        assert profiled.sequence_length == plain.sequence_length == prefill + step + 1
+        s = plain.sequence_length
+        for a, b in ((plain._key_codes, profiled._key_codes), (plain._value_codes, profiled._value_codes)):
+            np.testing.assert_array_equal(a[:, :, :s].cpu().numpy(), b[:, :, :s].cpu().numpy())
+    assert all(t >= 0.0 for t in profiled.last_decode_profile.values())
+
+
 @pytest.mark.parametrize("seq_len", [1, 7, 255, 256, 257, 1000, 4097])
 def test_ragged_lengths_and_split_invariance(hip_device, seq_len):
     import torque_hip as th

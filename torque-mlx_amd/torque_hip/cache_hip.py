@@ -13,7 +13,10 @@ Strategies: "split_batched" (default) and "auto" use the split-K kernel with
 the default split count; "fused_per_head" uses the same kernel with one split
 per head group.  With ``profile_decode_components`` the decode is run as the
 reference's three stages (score kernel, softmax kernel, value kernel), each
-timed with HIP events into ``last_decode_profile``.
+timed with HIP events into ``last_decode_profile``; ``decode_with_current``
+and ``decode_append`` then run the reference's staged path with the current
+token (its score and value share timed as ``tail_seconds``; decode_append as
+that decode followed by the append, ``append_seconds``).
 """
 
 from __future__ import annotations
@@ -177,14 +180,17 @@ class TorqueKVCacheHIP:
             rotate_values=self.rotate_values_on_append,
         )
         profile = self.last_decode_profile if self.profile_decode_components else None
-        with EventTimer(profile, "packed_decode_seconds", self._store.device):
-            outputs = self._store.decode(
-                queries,
-                rotate_query=self.rotate_queries_on_decode,
-                inverse_output=not self.config.fused_weights,
-                current=current,
-                n_splits=self._n_splits(),
-            )
+        if self._staged_profile(profile):
+            outputs = self._decode_with_current_staged(queries, current, profile)
+        else:
+            with EventTimer(profile, "packed_decode_seconds", self._store.device):
+                outputs = self._store.decode(
+                    queries,
+                    rotate_query=self.rotate_queries_on_decode,
+                    inverse_output=not self.config.fused_weights,
+                    current=current,
+                    n_splits=self._n_splits(),
+                )
         return self._finalize_output(outputs, query_heads=query_heads, return_numpy=return_numpy)
 
     decode_mlx_with_current = decode_with_current
@@ -205,17 +211,28 @@ class TorqueKVCacheHIP:
         query_heads = int(queries.shape[1])
         self._check_groups(query_heads)
         profile = self.last_decode_profile if self.profile_decode_components else None
-        with EventTimer(profile, "packed_decode_seconds", self._store.device):
-            outputs = self._store.decode_append(
-                queries,
-                keys,
-                values,
-                rotate_query=self.rotate_queries_on_decode,
-                inverse_output=not self.config.fused_weights,
-                rotate_keys=self.rotate_keys_on_append,
-                rotate_values=self.rotate_values_on_append,
-                n_splits=self._n_splits(),
+        if self._staged_profile(profile):
+            # profiling: the two calls this launch replaces, the decode staged as the reference times it
+            current = self._store.quantize_current(
+                keys, values, rotate_keys=self.rotate_keys_on_append, rotate_values=self.rotate_values_on_append
             )
+            outputs = self._decode_with_current_staged(queries, current, profile)
+            with EventTimer(profile, "append_seconds", self._store.device):
+                self._store.append(
+                    keys, values, rotate_keys=self.rotate_keys_on_append, rotate_values=self.rotate_values_on_append
+                )
+        else:
+            with EventTimer(profile, "packed_decode_seconds", self._store.device):
+                outputs = self._store.decode_append(
+                    queries,
+                    keys,
+                    values,
+                    rotate_query=self.rotate_queries_on_decode,
+                    inverse_output=not self.config.fused_weights,
+                    rotate_keys=self.rotate_keys_on_append,
+                    rotate_values=self.rotate_values_on_append,
+                    n_splits=self._n_splits(),
+                )
         self.sequence_length += 1
         return self._finalize_output(outputs, query_heads=query_heads, return_numpy=return_numpy)
 
@@ -259,10 +276,14 @@ class TorqueKVCacheHIP:
                 f"query head count {query_heads} must be divisible by kv_heads {self.config.kv_heads}",
             )
 
+    def _staged_profile(self, profile: dict[str, float] | None) -> bool:
+        """Profiling runs the reference's staged split path; it has no per-vector scales, so scaled
+        caches time the fused decode instead."""
+        return profile is not None and self.resolve_decode_strategy() == "split_batched" and not self._store.scaled
+
     def _decode_packed(self, queries: torch.Tensor) -> torch.Tensor:
         profile = self.last_decode_profile if self.profile_decode_components else None
-        # The three-stage profile has no per-vector scales: scaled caches time the fused decode.
-        if profile is not None and self.resolve_decode_strategy() == "split_batched" and not self._store.scaled:
+        if self._staged_profile(profile):
             return self._decode_staged(queries, profile)
         with EventTimer(profile, "packed_decode_seconds", self._store.device):
             return self._store.decode(
@@ -296,6 +317,51 @@ class TorqueKVCacheHIP:
             out_rot = ops.accumulate_packed_values_batched(
                 weights, v_rows, store.value_centroids, bit_width=cfg.bit_width, head_dim=cfg.head_dim
             )
+        if cfg.fused_weights:
+            out = out_rot
+        else:
+            with EventTimer(profile, "inverse_rotation_seconds", dev):
+                out = self.rotation.inverse_device(out_rot)
+        return out.reshape(num_layers, query_heads, cfg.head_dim)
+
+    def _decode_with_current_staged(
+        self, queries: torch.Tensor, current: tuple[torch.Tensor, torch.Tensor], profile: dict[str, float]
+    ) -> torch.Tensor:
+        """The reference's staged decode with one current token (cache_mlx.py:565-640), each stage timed:
+        the current token's score (tail_seconds), the packed scores, one softmax over the packed scores
+        and the current score, the packed value sum, the current value's share (tail_seconds)."""
+        cfg, store = self.config, self._store
+        dev = store.device
+        num_layers, query_heads = int(queries.shape[0]), int(queries.shape[1])
+        group = query_heads // cfg.kv_heads
+        with EventTimer(profile, "query_rotation_seconds", dev):
+            q_rot = self.rotation.apply_device(queries) if self.rotate_queries_on_decode else queries.float()
+        layer_idx = torch.arange(num_layers, device=dev).repeat_interleave(query_heads)
+        kv_idx = (torch.arange(query_heads, device=dev) // group).repeat(num_layers)
+        q_flat = q_rot.reshape(num_layers * query_heads, cfg.head_dim).contiguous()
+        cur_k, cur_v = current[0][layer_idx, kv_idx], current[1][layer_idx, kv_idx]  # [B, D], rotated, dequantized
+        with EventTimer(profile, "tail_seconds", dev):
+            current_scores = (cur_k * q_flat).sum(dim=1, keepdim=True)
+        s = store.length
+        if s == 0:
+            with EventTimer(profile, "tail_seconds", dev):
+                out_rot = cur_v.clone()
+        else:
+            k_rows = store.key_codes[layer_idx, kv_idx, :s]
+            v_rows = store.value_codes[layer_idx, kv_idx, :s]
+            with EventTimer(profile, "packed_score_seconds", dev):
+                scores = ops.score_packed_query_batched(
+                    q_flat, k_rows, store.key_centroids, bit_width=cfg.bit_width, head_dim=cfg.head_dim
+                )
+            with EventTimer(profile, "softmax_seconds", dev):
+                weights = ops.softmax_rows(torch.cat([scores, current_scores], dim=1), 1.0 / sqrt(cfg.head_dim))
+            with EventTimer(profile, "packed_value_seconds", dev):
+                packed_out = ops.accumulate_packed_values_batched(
+                    weights[:, :s].contiguous(), v_rows, store.value_centroids, bit_width=cfg.bit_width,
+                    head_dim=cfg.head_dim,
+                )
+            with EventTimer(profile, "tail_seconds", dev):
+                out_rot = packed_out + cur_v * weights[:, s:]
         if cfg.fused_weights:
             out = out_rot
         else:
