@@ -276,7 +276,7 @@ def read_ceiling(torch, _lib, hip, dev, step_bytes: int, total_mib: int) -> dict
         "full_pass_bytes": n_chunks * chunk,
         "gbps_step_bytes": round(step_bytes / (step_us * 1e-6) / 1e9, 1),
         "step_bytes": step_bytes,
-        "kernel": "stream_read_kernel (16-byte loads, 8 workgroups per CU)",
+        "kernel": "stream_read_kernel (nontemporal 16-byte loads, 4 in flight per thread, 512 threads, 1 workgroup per CU)",
     }
 
 

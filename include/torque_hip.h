@@ -265,8 +265,9 @@ int tq_accumulate_packed(const float* weights, const uint32_t* codes, int batch,
                          int bits, const float* centroids, float* out, hipStream_t stream);
 
 /* Measurement helper, no counterpart in the reference: streams `bytes` bytes
- * (a multiple of 16, 16-byte aligned) through 16-byte loads over n_blocks
- * workgroups (<= 0: eight per compute unit) -- the device's streaming-read
+ * (a multiple of 16, 16-byte aligned) through nontemporal 16-byte loads,
+ * four in flight per thread, over n_blocks workgroups of 512 threads (<= 0:
+ * one per compute unit) -- the device's streaming-read
  * ceiling that the decode kernels' bandwidth is compared with.  `sink` holds
  * n_blocks floats and is written only in the (practically impossible) case
  * that the xor of the data equals a fixed pattern.  start/stop events (may be

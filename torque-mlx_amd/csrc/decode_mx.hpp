@@ -240,13 +240,13 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
     const BufferRsrc rk = make_rsrc(kbase + static_cast<int64_t>(row0) * ROW, bytes);
     const BufferRsrc rv = make_rsrc(vbase + static_cast<int64_t>(row0) * ROW, bytes);
     if constexpr (KW == 2) {
-      const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(rk, koff, 0, 0);
+      const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(rk, koff, 0, kRowLoadPolicy);
       r.k[0] = x.x;
       r.k[1] = x.y;
     } else {
 #pragma unroll
       for (int q = 0; q < KW / 4; ++q) {
-        const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 16 * q, 0, 0);
+        const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 16 * q, 0, kRowLoadPolicy);
         r.k[4 * q] = x.x;
         r.k[4 * q + 1] = x.y;
         r.k[4 * q + 2] = x.z;
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
-      for (int q = 0; q < VW; ++q) r.v[rr][q] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + rr * ROW + 64 * q, 0, 0);
+      for (int q = 0; q < VW; ++q) r.v[rr][q] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + rr * ROW + 64 * q, 0, kRowLoadPolicy);
   };
 
   // ---- set-up loads first (centroids, query, signs, appended token), then

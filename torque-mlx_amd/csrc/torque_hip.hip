@@ -427,8 +427,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int off = (wave * TPW + u * TPB + gi) * 4;
-      ks[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rk, off, 0, 0));
-      vs[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0));
+      ks[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rk, off, 0, kRowLoadPolicy));
+      vs[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, kRowLoadPolicy));
     }
   };
   auto load_iter = [&](int i, Raw (&kr)[U], Raw (&vr)[U], float (&ks)[U], float (&vs)[U]) {
@@ -1162,20 +1162,31 @@ __global__ __launch_bounds__(kBlock) void accumulate_kernel(const float* __restr
 // ============================================================== measurement
 
 
-// Streaming read of n16 16-byte words, four loads in flight per thread.  The
-// store happens only if the xor of everything read equals a fixed pattern,
-// which keeps the loads live without writing in practice.
-__global__ __launch_bounds__(kBlock) void stream_read_kernel(const uint4* __restrict__ p, int64_t n16,
-                                                             float* __restrict__ sink) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-  int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+constexpr int kStreamThreads = 512;  // streaming-read probe: 512 threads, one workgroup per CU
+
+// Streaming-read probe (the bench's HBM ceiling): every thread keeps four
+// nontemporal 16-byte loads in flight over a grid-stride pass.  The shape is
+// the best of a sweep on MI355X (grid-stride and per-workgroup chunks; 1, 2,
+// 4, 8, 16 loads in flight; 256 / 512 / 1024 threads; 1-16 workgroups per
+// CU; with and without the nontemporal bit): 6.9-7.0 TB/s over a 768 MiB
+// pass, against 6.3-6.5 for the best cached-load shapes.  The store happens
+// only if the xor of everything read equals a fixed pattern, which keeps the
+// loads live without writing in practice.
+__global__ __launch_bounds__(kStreamThreads) void stream_read_kernel(const uint4* __restrict__ p, int64_t n16,
+                                                                     float* __restrict__ sink) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4* q = reinterpret_cast<const u32x4*>(p);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kStreamThreads;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * kStreamThreads + threadIdx.x;
   uint32_t acc = 0;
   for (; i + 3 * stride < n16; i += 4 * stride) {
-    const uint4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
-    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+    const u32x4 a = __builtin_nontemporal_load(q + i), b = __builtin_nontemporal_load(q + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(q + i + 2 * stride), d = __builtin_nontemporal_load(q + i + 3 * stride);
+    const u32x4 x = a ^ b ^ c ^ d;
+    acc ^= x.x ^ x.y ^ x.z ^ x.w;
   }
   for (; i < n16; i += stride) {
-    const uint4 a = p[i];
+    const u32x4 a = __builtin_nontemporal_load(q + i);
     acc ^= a.x ^ a.y ^ a.z ^ a.w;
   }
   if (acc == 0x9E3779B9u) sink[blockIdx.x] = 1.f;
@@ -2211,14 +2222,14 @@ int tq_stream_read(const void* data, size_t bytes, float* sink, int n_blocks, hi
   if (data == nullptr || sink == nullptr) return fail(TQ_ERR_BAD_ARG, "data and sink must be non-null");
   if (bytes % 16 != 0 || reinterpret_cast<uintptr_t>(data) % 16 != 0)
     return fail(TQ_ERR_BAD_ARG, "bytes and the data address must be multiples of 16");
-  if (n_blocks <= 0) n_blocks = 8 * device_cu_count();
+  if (n_blocks <= 0) n_blocks = device_cu_count();
   const int64_t n16 = static_cast<int64_t>(bytes / 16);
   if (start != nullptr || stop != nullptr)
-    hipExtLaunchKernelGGL(stream_read_kernel, dim3(n_blocks), dim3(kBlock), 0, stream, start, stop, 0,
+    hipExtLaunchKernelGGL(stream_read_kernel, dim3(n_blocks), dim3(kStreamThreads), 0, stream, start, stop, 0,
                           static_cast<const uint4*>(data), n16, sink);
   else
-    hipLaunchKernelGGL(stream_read_kernel, dim3(n_blocks), dim3(kBlock), 0, stream, static_cast<const uint4*>(data),
-                       n16, sink);
+    hipLaunchKernelGGL(stream_read_kernel, dim3(n_blocks), dim3(kStreamThreads), 0, stream,
+                       static_cast<const uint4*>(data), n16, sink);
   return launch_status("stream_read_kernel");
 }
 

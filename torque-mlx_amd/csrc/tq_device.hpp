@@ -313,6 +313,12 @@ __device__ __forceinline__ uint32_t unpack_code(const uint32_t* __restrict__ row
 // memory, so rows past the end of a range need no clamp.  Untyped loads on
 // this target take DATA_FORMAT = 32 bits in the descriptor's last word.
 constexpr int kBufferWord3 = 0x00020000;
+// Cache policy of the K/V row loads: nontemporal (the `nt` bit).  A decode
+// reads every row once per call, so the rows should not displace what stays
+// cached between launches (the per-split partials the merge kernel reads
+// next): measured at M, 16.5 -> 15.7 us per step with the same split-kernel
+// time; at C4 30.8 -> 29.7.
+constexpr int kRowLoadPolicy = 2;
 using BufferRsrc = __amdgpu_buffer_rsrc_t;
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -344,7 +350,7 @@ struct PackedB4 {
   }
   __device__ static int slice_offset(int slice) { return 8 * slice; }
   __device__ static Raw load(BufferRsrc r, int off) {
-    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kRowLoadPolicy);
     return {v.x, v.y};
   }
   __device__ static void decode(const Raw& r, int /*slice*/, const LutT* __restrict__ lut, float (&x)[kSliceDims]) {
@@ -381,7 +387,7 @@ struct PackedB2 {
     return {*reinterpret_cast<const uint32_t*>(row + 4 * slice)};
   }
   __device__ static int slice_offset(int slice) { return 4 * slice; }
-  __device__ static Raw load(BufferRsrc r, int off) { return {__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)}; }
+  __device__ static Raw load(BufferRsrc r, int off) { return {__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kRowLoadPolicy)}; }
   __device__ static void decode(const Raw& r, int /*slice*/, const LutT* __restrict__ lut, float (&x)[kSliceDims]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -418,7 +424,7 @@ struct PackedB3 {
   }
   __device__ static int slice_offset(int slice) { return 4 * ((3 * slice) >> 1); }
   __device__ static Raw load(BufferRsrc r, int off) {
-    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kRowLoadPolicy);
     return {v.x, v.y};
   }
   __device__ static void decode(const Raw& r, int slice, const LutT* __restrict__ lut, float (&x)[kSliceDims]) {
@@ -453,7 +459,7 @@ struct DenseF16 {
   }
   __device__ static int slice_offset(int slice) { return 16 * slice; }
   __device__ static Raw load(BufferRsrc r, int off) {
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kRowLoadPolicy);
     return {make_uint4(v.x, v.y, v.z, v.w)};
   }
   __device__ static void decode(const Raw& r, int, const LutT*, float (&x)[kSliceDims]) {
@@ -487,7 +493,7 @@ struct DenseF32 {
   }
   __device__ static int slice_offset(int slice) { return 16 * slice; }
   __device__ static Raw load(BufferRsrc r, int off) {
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kRowLoadPolicy);
     return {make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w))};
   }
   __device__ static void decode(const Raw& r, int, const LutT*, float (&x)[kSliceDims]) {
