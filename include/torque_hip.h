@@ -225,7 +225,11 @@ int tq_decode_append(const void* query, int query_dtype, const void* new_keys, c
 
 /* Same as tq_decode; start/stop events (may be NULL) are bound to the split
  * kernel itself, so hipEventElapsedTime gives its execution time (the merge
- * kernel, when launched, follows it on the stream). */
+ * kernel, when launched, follows it on the stream).  When either event is
+ * given, the merge launch is profiled as well, with a pair of events the
+ * library owns (one pair per device): a dispatch with profiling that follows
+ * one without starts late on most of the GPU's XCDs, and the split kernel's
+ * events would count that delay as its own time. */
 int tq_decode_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
                     int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
                     int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,

@@ -1412,7 +1412,8 @@ struct AppendSpec {
 
 int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hipStream_t stream, hipEvent_t start,
                 hipEvent_t stop);
-int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream);
+int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream,
+                 bool profiled);
 
 template <int D, bool QF16>
 void launch_mx_t(const DecodeArgs& a, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
@@ -1564,7 +1565,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   if (rc) return rc;
   rc = launch_status("decode_kernel");
   if (rc || p.n_splits == 1) return rc;
-  return launch_merge(m, num_layers, query_heads, head_dim, stream);
+  return launch_merge(m, num_layers, query_heads, head_dim, stream, start != nullptr || stop != nullptr);
 }
 
 int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hipStream_t stream, hipEvent_t start,
@@ -1592,18 +1593,70 @@ int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hi
   return rc;
 }
 
-int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream) {
+// Events of the merge launch of a timed call, one pair per device (created on
+// first use with that device current; never read).  A timed call launches
+// the merge kernel with profiling too: a dispatch launched with profiling
+// events right after one launched without starts on six of the eight XCDs
+// about 1.2 us after the other two (measured on MI355X for the split kernel
+// after an unprofiled merge: median workgroup start skew 1.25 us, against
+// 0.13 us with no events and 0.15 us with every dispatch profiled), and the
+// split kernel's events would count that delay as its own time.
+struct ProfileEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+std::mutex g_profile_mutex;
+ProfileEvents g_merge_events[kMaxDevices];
+
+int merge_profile_events(ProfileEvents* ev) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TQ_ERR_LAUNCH, std::string("no current HIP device: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(TQ_ERR_UNSUPPORTED, "device index " + std::to_string(dev) + " out of range");
+  std::lock_guard<std::mutex> lock(g_profile_mutex);
+  ProfileEvents& p = g_merge_events[dev];
+  if (p.start == nullptr) {
+    hipEvent_t a = nullptr, b = nullptr;
+    hipError_t r = hipEventCreate(&a);
+    if (r == hipSuccess) r = hipEventCreate(&b);
+    if (r != hipSuccess) {
+      if (a != nullptr) (void)hipEventDestroy(a);
+      return fail(TQ_ERR_LAUNCH, std::string("hipEventCreate failed: ") + hipGetErrorString(r));
+    }
+    p.start = a;
+    p.stop = b;
+  }
+  *ev = p;
+  return TQ_OK;
+}
+
+template <int D>
+void launch_merge_d(const MergeArgs& m, unsigned mblk, hipStream_t stream, const ProfileEvents* ev) {
+  if (ev != nullptr)
+    hipExtLaunchKernelGGL(merge_kernel<D>, dim3(mblk), dim3(kBlock), 0, stream, ev->start, ev->stop, 0, m);
+  else
+    hipLaunchKernelGGL(merge_kernel<D>, dim3(mblk), dim3(kBlock), 0, stream, m);
+}
+
+int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream,
+                 bool profiled) {
   const unsigned mblk =
       static_cast<unsigned>(static_cast<int64_t>(num_layers) * query_heads * (head_dim / kMergeDims));
+  ProfileEvents ev;
+  if (profiled) {
+    const int rc = merge_profile_events(&ev);
+    if (rc) return rc;
+  }
+  const ProfileEvents* evp = profiled ? &ev : nullptr;
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL(merge_kernel<64>, dim3(mblk), dim3(kBlock), 0, stream, m);
+      launch_merge_d<64>(m, mblk, stream, evp);
       break;
     case 128:
-      hipLaunchKernelGGL(merge_kernel<128>, dim3(mblk), dim3(kBlock), 0, stream, m);
+      launch_merge_d<128>(m, mblk, stream, evp);
       break;
     default:
-      hipLaunchKernelGGL(merge_kernel<256>, dim3(mblk), dim3(kBlock), 0, stream, m);
+      launch_merge_d<256>(m, mblk, stream, evp);
       break;
   }
   return launch_status("merge_kernel");
