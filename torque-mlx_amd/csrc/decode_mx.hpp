@@ -59,7 +59,9 @@
 // pairs whatever the codes (measured: 2.96 cycles per wave read against 6.6
 // for one shared 2 KB table).  The key table sits at LDS byte 0, the value
 // table at 65536, so a lookup address is one v_perm_b32 that puts the code
-// byte in bits 8..15 of the lane's base.
+// byte in bits 8..15 of the lane's base.  Wavefronts 4..11 write the tables
+// straight from the 32 centroids (held one per lane) while wavefronts 0..3
+// prepare the queries; one barrier ends the set-up.
 
 namespace mx {
 
@@ -83,14 +85,12 @@ struct Smem {
   static constexpr int kQBytes = 4 * D * 4;           // float32 scaled query [4][D]
   static constexpr int kCurBytes = 2 * D * 4 + 2 * D;  // append mode: s_cur [2][D] + codes [2][D]
   static constexpr int kMisc = 1024;
-  static constexpr int kStageBytes = 2 * 256 * 8;       // one copy of each table, staged before replication
   static constexpr int kRedBytes = kWaves * 4 * (D + 10) * 4;  // after the loop, inside the table area
   static constexpr int kQb = 2 * kTableBytes;
   static constexpr int kQ = kQb + kQbBytes;
   static constexpr int kCur = kQ + kQBytes;
   static constexpr int kMiscOff = kCur + kCurBytes;
-  static constexpr int kStage = kMiscOff + kMisc;
-  static constexpr int kTotal = kStage + kStageBytes;
+  static constexpr int kTotal = kMiscOff + kMisc;
   static_assert(kRedBytes + 2 * kWaves * 4 * 4 <= 2 * kTableBytes, "reduction fits in the table area");
 };
 
@@ -147,29 +147,29 @@ __device__ __forceinline__ uint2 table_entry(float ce0, float ce1, int sh, bool 
   return key ? make_uint2(pack_f16x2(h0, h1), pack_f16x2(l0, l1)) : make_uint2(pack_f16x2(h0, l0), pack_f16x2(h1, l1));
 }
 
-// Replicates the staged entries (stage[t][e], t = 0 keys, 1 values) into the
-// two 64 KB tables, in 128 spans of 1 KB: wavefront w writes spans w,
-// w + kWaves, ..., lane l the 16 bytes (two copies) at 1 KB * span + 16 l.
-// Each write instruction covers 1 KB contiguously (no bank conflicts) and its
-// lanes read 4 distinct staged entries (broadcast reads).
-__device__ __forceinline__ void replicate_tables(uint8_t* smem, const uint2* stage, int wave, int lane) {
+// Writes both tables from the centroids: writer wavefront w (0..7) fills the
+// 1 KB spans w, w + 8, ..., w + 120; in span s lane l writes the 16 bytes at
+// 1 KB * s + 16 l, two copies of entry e = 4 (s % 64) + l / 16 of table
+// s / 64 (keys, then values).  The entry's centroids are c[e % 16] =
+// c[4 (s % 4) + l / 16], fixed for the wavefront (s % 4 = w % 4), and
+// c[e / 16] = c[(s / 4) % 16], uniform over the span.  cvec: lane j < 16
+// holds key centroid j, lane 16 + j value centroid j.  Each write covers
+// 1 KB contiguously (no bank conflicts).
+constexpr int kTableWriters = 8;
+__device__ __forceinline__ void write_tables(uint8_t* smem, float cvec, int sh_k, int sh_v, int w, int lane) {
   constexpr int kSpans = 2 * kTableBytes / 1024;
-  constexpr int kSteps = (kSpans + kWaves - 1) / kWaves;
-  // All reads before all writes: the compiler cannot tell the staged entries
-  // from the tables (one shared array), so interleaving would serialize
-  // every read behind the previous write.
-  uint2 v[kSteps];
+  constexpr int kPer = kSpans / kTableWriters;
+  static_assert(kSpans % kTableWriters == 0 && kPer % 2 == 0, "spans split evenly, keys then values");
+  const int src0 = 4 * (w & 3) + (lane >> 4);
+  const float c0k = __shfl(cvec, src0), c0v = __shfl(cvec, 16 + src0);
+  const int cbits = __builtin_bit_cast(int, cvec);
 #pragma unroll
-  for (int k = 0; k < kSteps; ++k) {
-    const int span = min(wave + k * kWaves, kSpans - 1);  // a wavefront past the end rewrites the last span
-    const int off = (span << 10) + (lane << 4);
-    v[k] = stage[((off >> 16) << 8) + ((off >> 8) & 255)];
-  }
-#pragma unroll
-  for (int k = 0; k < kSteps; ++k) {
-    const int span = min(wave + k * kWaves, kSpans - 1);
-    const int off = (span << 10) + (lane << 4);
-    *reinterpret_cast<uint4*>(smem + off) = make_uint4(v[k].x, v[k].y, v[k].x, v[k].y);
+  for (int k = 0; k < kPer; ++k) {
+    const int span = w + kTableWriters * k;
+    const bool key = k < kPer / 2;
+    const float c1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(cbits, (key ? 0 : 16) + ((span >> 2) & 15)));
+    const uint2 e = table_entry(key ? c0k : c0v, c1, key ? sh_k : sh_v, key);
+    *reinterpret_cast<uint4*>(smem + (span << 10) + (lane << 4)) = make_uint4(e.x, e.y, e.x, e.y);
   }
 }
 
@@ -262,11 +262,9 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   // ---- set-up loads first (centroids, query, signs, appended token), then
   // the first tiles' rows: vector loads return in order, so a set-up value
   // requested after the rows would wait for them.
-  const float* cent_t = tid < 256 ? a.cent_k : a.cent_v;  // thread t stages entry t & 255 of table t / 256
-  const float ce0 = cent_t[tid & 15], ce1 = cent_t[(tid >> 4) & 15];
-  // power-of-two scale of this wavefront's table (key table for waves 0..3):
-  // the 16 lanes of a row hold all 16 centroids in ce0
-  const int sh_t = scale_shift(group_reduce<16, OpMax>(fabsf(ce0)));
+  // centroids in lanes: lane j < 16 key centroid j, lane 16 + j value centroid j
+  const float* cptr = lane < 16 ? a.cent_k + lane : a.cent_v + (lane & 15);
+  const float cvec = lane < 32 ? *cptr : 0.f;
   const bool appending = a.new_k != nullptr;
   const bool appender = appending && split == 0 && wave < 2;
   constexpr int kLevels = 15;
@@ -299,11 +297,13 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   constexpr int NR = kPrefetch + 1;
   Raw ring[NR];
   int kq[NR];  // tile held by each ring slot (wavefront-uniform)
+  auto prefetch = [&]() {
 #pragma unroll
-  for (int j = 0; j < kPrefetch; ++j) {
-    kq[j] = j * kWaves + wave;
-    load_tile(kq[j], ring[j]);
-  }
+    for (int j = 0; j < kPrefetch; ++j) {
+      kq[j] = j * kWaves + wave;
+      load_tile(kq[j], ring[j]);
+    }
+  };
   int* s_claim = reinterpret_cast<int*>(s_misc + 8);
   if (tid == 0) *s_claim = kPrefetch * kWaves;  // first dynamic claim; read only after the set-up barriers
   // lane 0 takes the next tile; the value is read (readfirstlane) only where
@@ -314,9 +314,12 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
     return k;
   };
 
-  uint2* s_stage = reinterpret_cast<uint2*>(smem + L::kStage);  // [2][256]
-  if (tid < 512) s_stage[tid] = table_entry(ce0, ce1, sh_t, tid < 256);  // stage[0][*] keys, stage[1][*] values
-  if (wave == 4 && lane == 0) s_misc[4] = ldexpf(1.f, -(sh_t + 7));  // weights carry 2^7, values 2^sh_v
+  // power-of-two scales of the two tables (lane rows 0 and 1 hold their centroids)
+  const int sh_lane = scale_shift(group_reduce<16, OpMax>(fabsf(cvec)));
+  const int sh_k = __builtin_amdgcn_readlane(sh_lane, 0), sh_v = __builtin_amdgcn_readlane(sh_lane, 16);
+  static_assert(kWaves - 4 == kTableWriters, "wavefronts 4.. write the tables");
+  if (wave >= 4) write_tables(smem, cvec, sh_k, sh_v, wave - 4, lane);
+  if (wave == 4 && lane == 0) s_misc[4] = ldexpf(1.f, -(sh_v + 7));  // weights carry 2^7, values 2^sh_v
 
   // ---- append mode: rotate (as on append) and quantize the new token.
   if (appender) {
@@ -351,11 +354,16 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
       s_qb[wave * L::kQbStride + lane * E + i] = __builtin_bit_cast(uint16_t, h);
       s_qb[(4 + wave) * L::kQbStride + lane * E + i] = __builtin_bit_cast(uint16_t, l);
     }
-    if (lane == 0) s_misc[wave] = ldexpf(1.f, -(sh_q + sh_t));  // raw score -> log2 units
+    if (lane == 0) s_misc[wave] = ldexpf(1.f, -(sh_q + sh_k));  // raw score -> log2 units
   }
-  __syncthreads();
-  replicate_tables(smem, s_stage, wave, lane);
-  __syncthreads();
+  // The rows go out after each wavefront's set-up work: with every CU's
+  // prefetch in flight the memory pipeline is full, and a wavefront whose
+  // next load cannot issue stalls, so loads issued first would hold the
+  // set-up back.
+  prefetch();
+  // the set-up exchanges data through LDS only: the barrier leaves the
+  // prefetched rows in flight
+  lds_barrier();
   if (appender) {
     constexpr int W = D * 4 / 32;
     if (hg == 0 && lane < W) {

@@ -531,7 +531,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < E; ++i) s_q[wave][lane * E + i] = qe[i] * a.q_scale;
   }
-  __syncthreads();
+  lds_barrier();  // LDS-only exchange: the prefetched rows stay in flight
   if constexpr (Fmt::kHasLut) {
     if (appender) {
       // Dequantized values through the centroid table (entry c holds centroid

@@ -29,6 +29,18 @@ __device__ __forceinline__ float to_f32<__half>(__half v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier that publishes LDS writes only: it waits for the
+// wavefront's LDS operations (lgkmcnt) and not for its outstanding global
+// loads.  __syncthreads() fences global memory as well, which waits for every
+// load in flight (vmcnt counts loads), so a barrier placed after a row
+// prefetch would hold each wavefront until its prefetched rows had landed.
+// Use it only where the wavefronts exchange data through LDS alone.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---------------------------------------------------------------------------
 // Cross-lane data movement without LDS.
 //
