@@ -58,7 +58,8 @@ def test_host_only_entry_points():
     assert _lib.split_kernel(8, 32, 64, 4, 0, _lib.TQ_F32) == "decode_mx_kernel<64,false>"
     assert _lib.split_kernel(8, 32, 128, 4, _lib.TQ_F32_PRODUCTS, _lib.TQ_F16) == "decode_kernel<PackedB4,128,4>"
     assert _lib.split_kernel(8, 32, 128, 2, 0, _lib.TQ_F16) == "decode_kernel<PackedB2,128,4>"
-    assert _lib.split_kernel(2, 8, 256, 4, 0, _lib.TQ_F16) == "decode_kernel<PackedB4,256,4>"
+    assert _lib.split_kernel(2, 8, 256, 4, 0, _lib.TQ_F16) == "decode_mx_kernel<256,true>"
+    assert _lib.split_kernel(2, 8, 256, 4, _lib.TQ_F32_PRODUCTS, _lib.TQ_F16) == "decode_kernel<PackedB4,256,4>"
     assert _lib.split_kernel(4, 8, 128, 4, 0, _lib.TQ_F16) == "decode_kernel<PackedB4,128,2>"
     with pytest.raises(ValueError):
         _lib.split_kernel(8, 30, 128, 4, 0, _lib.TQ_F16)

@@ -37,6 +37,7 @@ def _codes(cache):
         (3, 64, 1, 4, 4, 300),
         (2, 256, 1, 2, 2, 513),
         (4, 256, 1, 1, 1, 5),
+        (4, 256, 1, 2, 4, 300),
         (4, 64, 1, 2, 8, 2100),
         (3, 128, 1, 3, 3, 1000),
     ],

@@ -1,4 +1,4 @@
-"""The matrix-core split kernel (4-bit rows, groups of 4 query heads, head_dim 64 / 128).
+"""The matrix-core split kernel (4-bit rows, groups of 4 query heads, head_dim 64 / 128 / 256).
 
 It forms every product from exact float16 hi/lo splits and sums in float32, so
 it must agree with the float32-product kernel (TQ_F32_PRODUCTS) to float32
@@ -88,6 +88,11 @@ CASES = [
     (64, 2, 4, 17, None),
     (64, 4, 4, 2100, None),
     (64, 2, 8, 4097, 3),
+    (256, 2, 4, 1, None),
+    (256, 2, 4, 17, None),
+    (256, 1, 4, 3000, None),
+    (256, 2, 4, 5000, 7),
+    (256, 2, 8, 2100, 3),
 ]
 
 
@@ -131,14 +136,15 @@ def test_matrix_kernel_large_score_range(hip_device, q_scale):
         assert err_mx < 2e-3  # the north-star bound (max-abs 2e-3 at unit-scale outputs)
 
 
-def test_matrix_kernel_rotation_and_current_token(hip_device):
+@pytest.mark.parametrize("head_dim", [128, 256])
+def test_matrix_kernel_rotation_and_current_token(hip_device, head_dim):
     """Query rotation, inverse output rotation and the current-token path agree with the float32
     kernel (both run the same epilogue arithmetic on different split products)."""
-    geo = dict(layers=1, kv_heads=2, group=4, head_dim=128, seq_len=700)
+    geo = dict(layers=1, kv_heads=2, group=4, head_dim=head_dim, seq_len=700)
     c = _case(11, capacity=800, q_dtype=torch.float16, q_scale=1.0, dev=hip_device, **geo)
     gen = torch.Generator(device=hip_device).manual_seed(3)
-    cur = (torch.randn((1, 2, 128), generator=gen, device=hip_device) * 0.5,
-           torch.randn((1, 2, 128), generator=gen, device=hip_device) * 0.05)
+    cur = (torch.randn((1, 2, head_dim), generator=gen, device=hip_device) * 0.5,
+           torch.randn((1, 2, head_dim), generator=gen, device=hip_device) * 0.05)
     for ns in (None, 1, 5):
         for current in (None, cur):
             mx = _decode(c, capacity=800, f32_products=False, n_splits=ns, rotate=True, current=current, **geo)

@@ -68,8 +68,18 @@ namespace mx {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 12;                // wavefronts per workgroup (3 per SIMD)
-constexpr int kThreads = kWaves * kWave;  // 768: one workgroup per compute unit
+// Wavefronts per workgroup (one workgroup per compute unit): 12, three per
+// SIMD, at head_dim 64 / 128; 8, two per SIMD with up to 256 VGPRs each, at
+// head_dim 256, whose accumulators and query operands take twice the
+// registers.
+template <int D>
+constexpr int waves_of() {
+  return D == 256 ? 8 : 12;
+}
+template <int D>
+constexpr int threads_of() {
+  return waves_of<D>() * kWave;
+}
 constexpr int kTile = 16;                 // tokens per wavefront iteration
 constexpr int kTilesPerBlock = 8;
 constexpr int kStride = kTilesPerBlock * kTile;  // rows per block (the unit dealt out to the splits)
@@ -85,13 +95,15 @@ struct Smem {
   static constexpr int kQBytes = 4 * D * 4;           // float32 scaled query [4][D]
   static constexpr int kCurBytes = 2 * D * 4 + 2 * D;  // append mode: s_cur [2][D] + codes [2][D]
   static constexpr int kMisc = 1024;
-  static constexpr int kRedBytes = kWaves * 4 * (D + 10) * 4;  // after the loop, inside the table area
+  static constexpr int kNW = waves_of<D>();
+  static constexpr int kRS = D <= 128 ? D + 10 : D + 18;       // padded reduction row (floats)
+  static constexpr int kRedBytes = kNW * 4 * kRS * 4;           // after the loop, inside the table area
   static constexpr int kQb = 2 * kTableBytes;
   static constexpr int kQ = kQb + kQbBytes;
   static constexpr int kCur = kQ + kQBytes;
   static constexpr int kMiscOff = kCur + kCurBytes;
   static constexpr int kTotal = kMiscOff + kMisc;
-  static_assert(kRedBytes + 2 * kWaves * 4 * 4 <= 2 * kTableBytes, "reduction fits in the table area");
+  static_assert(kRedBytes + 2 * kNW * 4 * 4 <= 2 * kTableBytes, "reduction fits in the table area");
 };
 
 __device__ __forceinline__ uint32_t pack_f16x2(_Float16 lo, _Float16 hi) {
@@ -147,25 +159,25 @@ __device__ __forceinline__ uint2 table_entry(float ce0, float ce1, int sh, bool 
   return key ? make_uint2(pack_f16x2(h0, h1), pack_f16x2(l0, l1)) : make_uint2(pack_f16x2(h0, l0), pack_f16x2(h1, l1));
 }
 
-// Writes both tables from the centroids: writer wavefront w (0..7) fills the
-// 1 KB spans w, w + 8, ..., w + 120; in span s lane l writes the 16 bytes at
-// 1 KB * s + 16 l, two copies of entry e = 4 (s % 64) + l / 16 of table
-// s / 64 (keys, then values).  The entry's centroids are c[e % 16] =
-// c[4 (s % 4) + l / 16], fixed for the wavefront (s % 4 = w % 4), and
-// c[e / 16] = c[(s / 4) % 16], uniform over the span.  cvec: lane j < 16
-// holds key centroid j, lane 16 + j value centroid j.  Each write covers
-// 1 KB contiguously (no bank conflicts).
-constexpr int kTableWriters = 8;
+// Writes both tables from the centroids: writer wavefront w (0..W-1, W = 8
+// or 4) fills the 1 KB spans w, w + W, ..., w + 128 - W; in span s lane l
+// writes the 16 bytes at 1 KB * s + 16 l, two copies of entry
+// e = 4 (s % 64) + l / 16 of table s / 64 (keys, then values).  The entry's
+// centroids are c[e % 16] = c[4 (s % 4) + l / 16], fixed for the wavefront
+// (s % 4 = w % 4, W being a multiple of 4), and c[e / 16] = c[(s / 4) % 16],
+// uniform over the span.  cvec: lane j < 16 holds key centroid j, lane 16 + j
+// value centroid j.  Each write covers 1 KB contiguously (no bank conflicts).
+template <int W>
 __device__ __forceinline__ void write_tables(uint8_t* smem, float cvec, int sh_k, int sh_v, int w, int lane) {
   constexpr int kSpans = 2 * kTableBytes / 1024;
-  constexpr int kPer = kSpans / kTableWriters;
-  static_assert(kSpans % kTableWriters == 0 && kPer % 2 == 0, "spans split evenly, keys then values");
+  constexpr int kPer = kSpans / W;
+  static_assert(W % 4 == 0 && kSpans % W == 0 && kPer % 2 == 0, "spans split evenly, keys then values");
   const int src0 = 4 * (w & 3) + (lane >> 4);
   const float c0k = __shfl(cvec, src0), c0v = __shfl(cvec, 16 + src0);
   const int cbits = __builtin_bit_cast(int, cvec);
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    const int span = w + kTableWriters * k;
+    const int span = w + W * k;
     const bool key = k < kPer / 2;
     const float c1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(cbits, (key ? 0 : 16) + ((span >> 2) & 15)));
     const uint2 e = table_entry(key ? c0k : c0v, c1, key ? sh_k : sh_v, key);
@@ -176,7 +188,8 @@ __device__ __forceinline__ void write_tables(uint8_t* smem, float cvec, int sh_k
 }  // namespace mx
 
 template <int D, bool QF16>
-__global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_mx_kernel(
+__global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
+    amdgpu_waves_per_eu(mx::waves_of<D>() / 4, mx::waves_of<D>() / 4))) void decode_mx_kernel(
     const DecodeArgs a) {
   using namespace mx;
   static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128 or 256");
@@ -187,6 +200,15 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   constexpr int NV = D / 16;          // value products per tile
   constexpr int VW = D == 256 ? 2 : 1;  // value dwords per lane per row
   constexpr int E = D / kWave;
+  constexpr int NW = waves_of<D>();   // wavefronts
+  // A row is processed in NH halves at head_dim 256 (key lookups and score
+  // products of dims [0, 128) then [128, 256) of each lane's quarter row;
+  // value lookups and products of dims [0, 128) then [128, 256)), so that
+  // only half a tile's lookups are live at a time.
+  constexpr int NH = D == 256 ? 2 : 1;
+  constexpr int KBH = KB / NH;        // key bytes (lookups) per half
+  constexpr int NSH = NS / NH;        // score products per half
+  constexpr int NVH = NV / NH;        // value products per half
   using L = Smem<D>;
 
   __shared__ __align__(16) uint8_t smem[L::kTotal];
@@ -210,7 +232,7 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   // s takes blocks s, s + n, s + 2n, ...), each block cut into
   // kTilesPerBlock tiles of 16 rows.  Tile k of this split is tile
   // k % kTilesPerBlock of its (k / kTilesPerBlock)-th block.  Wavefronts
-  // claim tiles: the first kPrefetch rounds statically (tile j * kWaves +
+  // claim tiles: the first kPrefetch rounds statically (tile j * NW +
   // wave), then from a counter in LDS, so a wavefront that runs ahead takes
   // more tiles and all finish within about a tile of each other.  Row offsets
   // are 32-bit (the host keeps capacity * ROW < 2^31).
@@ -300,12 +322,12 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   auto prefetch = [&]() {
 #pragma unroll
     for (int j = 0; j < kPrefetch; ++j) {
-      kq[j] = j * kWaves + wave;
+      kq[j] = j * NW + wave;
       load_tile(kq[j], ring[j]);
     }
   };
   int* s_claim = reinterpret_cast<int*>(s_misc + 8);
-  if (tid == 0) *s_claim = kPrefetch * kWaves;  // first dynamic claim; read only after the set-up barriers
+  if (tid == 0) *s_claim = kPrefetch * NW;  // first dynamic claim; read only after the set-up barrier
   // lane 0 takes the next tile; the value is read (readfirstlane) only where
   // the tile is loaded, one iteration later, so the atomic's latency hides
   auto claim = [&]() {
@@ -317,8 +339,7 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   // power-of-two scales of the two tables (lane rows 0 and 1 hold their centroids)
   const int sh_lane = scale_shift(group_reduce<16, OpMax>(fabsf(cvec)));
   const int sh_k = __builtin_amdgcn_readlane(sh_lane, 0), sh_v = __builtin_amdgcn_readlane(sh_lane, 16);
-  static_assert(kWaves - 4 == kTableWriters, "wavefronts 4.. write the tables");
-  if (wave >= 4) write_tables(smem, cvec, sh_k, sh_v, wave - 4, lane);
+  if (wave >= 4) write_tables<NW - 4>(smem, cvec, sh_k, sh_v, wave - 4, lane);
   if (wave == 4 && lane == 0) s_misc[4] = ldexpf(1.f, -(sh_v + 7));  // weights carry 2^7, values 2^sh_v
 
   // ---- append mode: rotate (as on append) and quantize the new token.
@@ -409,15 +430,17 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   //   score products(i + 1)
   // (the key reads have the softmax and value products to land, the value
   // reads the score products and the next iteration's first half).
-  uint2 kl[KB];      // key lookups, one per byte of the lane's quarter row
-  uint2 vl[NV][2];   // value lookups: product j, token pair (0, 1) / (2, 3)
-  auto key_lookups = [&](const Raw& r) {
+  uint2 kl[KBH];      // key lookups of one half, one per byte of the lane's quarter row
+  uint2 vl[NVH][2];   // value lookups of one half: product j, token pair (0, 1) / (2, 3)
+  auto key_lookups = [&](const Raw& r, int h) {
 #pragma unroll
-    for (int b = 0; b < KB; ++b) kl[b] = lds_read_u2(smem, lut_addr_dyn(r.k[b / 4], base_k, b & 3));
+    for (int b = 0; b < KBH; ++b) kl[b] = lds_read_u2(smem, lut_addr_dyn(r.k[(h * KBH + b) / 4], base_k, b & 3));
   };
-  auto value_lookups = [&](const Raw& r) {
-#pragma unroll
-    for (int q = 0; q < VW; ++q) {
+  // value dword q = h of the lane's rows (dims 128 h + 8 n .. + 7; D = 64:
+  // the n & 1 half of dword n / 2)
+  auto value_lookups = [&](const Raw& r, int h) {
+    {
+      const int q = h;
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) {
         uint32_t w0 = r.v[2 * pr][q], w1 = r.v[2 * pr + 1][q];
@@ -429,18 +452,19 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
         const uint32_t ev = (w0 & 0x0f0f0f0fu) | ((w1 << 4) & 0xf0f0f0f0u);
         const uint32_t od = ((w0 >> 4) & 0x0f0f0f0fu) | (w1 & 0xf0f0f0f0u);
         constexpr int JN = D == 64 ? 4 : 8;  // dims per dword this lane uses
+        static_assert(JN == NVH, "one value product per dim of the dword");
 #pragma unroll
         for (int jj = 0; jj < JN; ++jj)
-          vl[q * 8 + jj][pr] = lds_read_u2(smem, lut_addr_dyn((jj & 1) ? od : ev, base_v, jj >> 1));
+          vl[jj][pr] = lds_read_u2(smem, lut_addr_dyn((jj & 1) ? od : ev, base_v, jj >> 1));
       }
     }
   };
-  auto scores = [&](f32x4v& ds) {
-    ds = f32x4v{0.f, 0.f, 0.f, 0.f};
+  auto scores = [&](f32x4v& ds, int h) {
 #pragma unroll
-    for (int s2 = 0; s2 < NS; ++s2) {
+    for (int s2 = 0; s2 < NSH; ++s2) {
+      const int q2 = 2 * (h * NSH + s2);
       const f16x8 A = as_f16x8(kl[2 * s2].x, kl[2 * s2].y, kl[2 * s2 + 1].x, kl[2 * s2 + 1].y);
-      const f16x8 B = as_f16x8(qd[2 * s2], qd[2 * s2], qd[2 * s2 + 1], qd[2 * s2 + 1]);
+      const f16x8 B = as_f16x8(qd[q2], qd[q2], qd[q2 + 1], qd[q2 + 1]);
       ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, ds, 0, 0, 0);
     }
   };
@@ -454,7 +478,7 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   // 4 + h their lo splits, each as an f16 pair (w, w) facing the value's
   // (hi, lo) k-slots.  Rows 8..15 carry junk weights whose output rows are
   // never read.  Only a split's last tiles can be partial.
-  auto values = [&](const f32x4v& ds, int k) {
+  auto softmax = [&](const f32x4v& ds, int k) {
     float s4[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) s4[rr] = ds[rr] + dpp_move<kDppRor12>(ds[rr]);
@@ -502,12 +526,14 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
     a2 = __builtin_amdgcn_update_dpp(a2, wlo, 0x104, 0xf, 0x2, false);              // row_shl:4 into lanes 4..7
     int a3 = __builtin_amdgcn_update_dpp(whi, whi, 0x10C, 0xf, 0x1, false);         // row_shl:12 into lanes 0..3
     a3 = __builtin_amdgcn_update_dpp(a3, wlo, 0x108, 0xf, 0x2, false);              // row_shl:8 into lanes 4..7
-    const f16x8 Aw = as_f16x8(static_cast<uint32_t>(a0), static_cast<uint32_t>(a1), static_cast<uint32_t>(a2),
-                              static_cast<uint32_t>(a3));
+    return as_f16x8(static_cast<uint32_t>(a0), static_cast<uint32_t>(a1), static_cast<uint32_t>(a2),
+                    static_cast<uint32_t>(a3));
+  };
+  auto value_products = [&](const f16x8& Aw, int h) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
+    for (int j = 0; j < NVH; ++j) {
       const f16x8 B = as_f16x8(vl[j][0].x, vl[j][0].y, vl[j][1].x, vl[j][1].y);
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aw, B, acc[j], 0, 0, 0);
+      acc[h * NVH + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aw, B, acc[h * NVH + j], 0, 0, 0);
     }
   };
 
@@ -524,11 +550,20 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
       kq[nx] = __builtin_amdgcn_readfirstlane(claimed);
       load_tile(kq[nx], ring[nx]);
       claimed = claim();
-      f32x4v ds;
-      key_lookups(ring[j]);
-      scores(ds);
-      value_lookups(ring[j]);
-      values(ds, kq[j]);
+      f32x4v ds = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        key_lookups(ring[j], h);
+        scores(ds, h);
+      }
+      value_lookups(ring[j], 0);
+      const f16x8 Aw = softmax(ds, kq[j]);
+      value_products(Aw, 0);
+#pragma unroll
+      for (int h = 1; h < NH; ++h) {
+        value_lookups(ring[j], h);
+        value_products(Aw, h);
+      }
       if (kq[(j + 1) % NR] >= n_tiles) {
         more = false;
         break;
@@ -539,18 +574,18 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   // ---- combine: rows h and 4 + h (lane groups 0 and 1), then the
   // wavefronts.  Lane n of group 0 holds head rr's output at dims of column n.
   __syncthreads();  // the tables are dead: reuse their space
-  // s_red: [kWaves x 4 heads] rows of RS floats; dim d of a row sits at
-  // d + 4 (d / 64), and RS = D + 10, so that the 32 lanes writing one
+  // s_red: [NW x 4 heads] rows of RS floats; dim d of a row sits at
+  // d + 4 (d / 64), and RS = 2 (mod 4) and above that, so that the 32 lanes writing one
   // register pair (16 dims x 2 rows) hit 32 distinct banks
-  constexpr int RS = D + 10;
+  constexpr int RS = L::kRS;
   float* s_red = reinterpret_cast<float*>(smem);
-  float* s_mw = reinterpret_cast<float*>(smem + kWaves * 4 * RS * 4);  // [kWaves][4]
-  float* s_lw = s_mw + kWaves * 4;                                     // [kWaves][4]
+  float* s_mw = reinterpret_cast<float*>(smem + NW * 4 * RS * 4);  // [NW][4]
+  float* s_lw = s_mw + NW * 4;                                       // [NW][4]
   auto red_pos = [](int d) { return d + 4 * (d >> 6); };
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    // dim of column n in product j: 8n + j (D = 128), 4n + j (D = 64)
-    const int dim = D == 64 ? 4 * n + j : 8 * n + j;
+    // dim of column n in product j: 128 (j / 8) + 8n + j % 8 (D = 128, 256), 4n + j (D = 64)
+    const int dim = D == 64 ? 4 * n + j : 128 * (j / 8) + 8 * n + (j % 8);
 #pragma unroll
     for (int pr = 0; pr < 2; ++pr) {
       // rows h (hi weights) and 4 + h (lo weights) of head h are lane groups
@@ -569,26 +604,26 @@ __global__ __launch_bounds__(mx::kThreads) __attribute__((amdgpu_waves_per_eu(3,
   }
   __syncthreads();
 
-  auto wave_weights = [&](int h, float (&f)[kWaves]) {
+  auto wave_weights = [&](int h, float (&f)[NW]) {
     float M = s_mw[h];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_mw[w * 4 + h]);
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, s_mw[w * 4 + h]);
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) f[w] = s_mw[w * 4 + h] == -INFINITY ? 0.f : fast_exp2(s_mw[w * 4 + h] - M);
+    for (int w = 0; w < NW; ++w) f[w] = s_mw[w * 4 + h] == -INFINITY ? 0.f : fast_exp2(s_mw[w * 4 + h] - M);
     return M;
   };
   if (wave < 4) {
-    float f[kWaves];
+    float f[NW];
     const float M = wave_weights(wave, f);
     float l = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) l = fmaf(s_lw[w * 4 + wave], f[w], l);
+    for (int w = 0; w < NW; ++w) l = fmaf(s_lw[w * 4 + wave], f[w], l);
     float e[E];
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       float v = 0.f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) v = fmaf(s_red[(w * 4 + wave) * RS + red_pos(lane * E + i)], f[w], v);
+      for (int w = 0; w < NW; ++w) v = fmaf(s_red[(w * 4 + wave) * RS + red_pos(lane * E + i)], f[w], v);
       e[i] = v * out_scale;
     }
     if (a.n_splits == 1) {

@@ -1305,7 +1305,7 @@ int decode_block_rows(int fmt, int head_dim) {
 }
 
 SplitKernel pick_kernel(int fmt, int head_dim, int hg, int flags) {
-  if (fmt == 4 && hg == 4 && (head_dim == 64 || head_dim == 128) && (flags & TQ_F32_PRODUCTS) == 0)
+  if (fmt == 4 && hg == 4 && (head_dim == 64 || head_dim == 128 || head_dim == 256) && (flags & TQ_F32_PRODUCTS) == 0)
     return SplitKernel::Mx;
   return SplitKernel::Fp32;
 }
@@ -1418,9 +1418,9 @@ int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_d
 template <int D, bool QF16>
 void launch_mx_t(const DecodeArgs& a, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (start != nullptr || stop != nullptr)
-    hipExtLaunchKernelGGL((decode_mx_kernel<D, QF16>), grid, dim3(mx::kThreads), 0, stream, start, stop, 0, a);
+    hipExtLaunchKernelGGL((decode_mx_kernel<D, QF16>), grid, dim3(mx::threads_of<D>()), 0, stream, start, stop, 0, a);
   else
-    hipLaunchKernelGGL((decode_mx_kernel<D, QF16>), grid, dim3(mx::kThreads), 0, stream, a);
+    hipLaunchKernelGGL((decode_mx_kernel<D, QF16>), grid, dim3(mx::threads_of<D>()), 0, stream, a);
 }
 
 template <int D>
@@ -1444,6 +1444,9 @@ int launch_mx(const DecodeArgs& a, int head_dim, hipStream_t stream, hipEvent_t 
       return TQ_OK;
     case 128:
       launch_mx_d<128>(a, grid, stream, start, stop);
+      return TQ_OK;
+    case 256:
+      launch_mx_d<256>(a, grid, stream, start, stop);
       return TQ_OK;
     default:
       return fail(TQ_ERR_UNSUPPORTED, "decode_mx_kernel: unsupported head dimension " + std::to_string(head_dim));
