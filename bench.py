@@ -305,7 +305,8 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
 
     stores = [c._store for c in caches]
     w = stores[0].layout.packed_words
-    matrix_kernel = _lib.split_kernel(hkv, hq, d, bits, 0, _lib.TQ_F16).startswith("decode_mx_kernel")
+    loop_kernel = _lib.split_kernel(hkv, hq, d, bits, 0, _lib.TQ_F16, s0 + steps)
+    matrix_kernel = loop_kernel.startswith("decode_mx_kernel")
     n_splits = [ops.plan_splits(1, hkv, hq, d, s0 + steps, dev, bit_width=bits) for _ in range(L)]
     ws = ops.workspace_for(1, hkv, hq, d, args.splits, dev)
     out = torch.empty((L, hq, d), dtype=torch.float32, device=dev)
@@ -451,6 +452,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
             "prefill": s0,
             "query_dtype": "f16",
             "n_splits_at_prefill": args.splits or n_splits[0],
+            "split_kernel": loop_kernel,
             "step": "per layer: tq_decode_append (pack the new token and decode with it) + merge kernel",
         },
         "step_us_mean": round(mean_us, 2),
@@ -623,7 +625,8 @@ def main() -> int:
     kern_us = float(np.mean(kern_ms) * 1e3)
     kern_med_us = float(np.median(kern_ms) * 1e3)
     achieved = algo_bytes / (kern_us * 1e-6) / 1e9
-    kernel_name = _lib.split_kernel(hkv, hq, d, bits, flags | (_lib.TQ_F32_PRODUCTS if scaled else 0), _lib.TQ_F16)
+    kernel_name = _lib.split_kernel(hkv, hq, d, bits, flags | (_lib.TQ_F32_PRODUCTS if scaled else 0), _lib.TQ_F16, s,
+                                    num_layers=L, n_splits=n_splits)
     matrix_kernel = kernel_name.startswith("decode_mx_kernel")
     if scaled:
         kernel_name += ",scaled"
@@ -648,7 +651,8 @@ def main() -> int:
         torch.cuda.synchronize()
         k32 = np.array([hip.elapsed_ms(a, b) for a, b in evs32]) * 1e3
         f32_products = {
-            "kernel": _lib.split_kernel(hkv, hq, d, bits, flags | _lib.TQ_F32_PRODUCTS, _lib.TQ_F16),
+            "kernel": _lib.split_kernel(hkv, hq, d, bits, flags | _lib.TQ_F32_PRODUCTS, _lib.TQ_F16, s,
+                                        num_layers=L, n_splits=n_f32),
             "n_splits": n_f32,
             "kernel_us_per_step": round(float(np.mean(k32)), 3),
             "kernel_us_median": round(float(np.median(k32)), 3),

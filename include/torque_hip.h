@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TQ_ABI_VERSION 2
+#define TQ_ABI_VERSION 3
 
 enum {
   TQ_OK = 0,
@@ -42,11 +42,15 @@ enum { TQ_F32 = 0, TQ_F16 = 1 };
 /* tq_append / tq_quantize_dequantize flags (reference cache_mlx.py:52-54) */
 enum { TQ_ROTATE_KEYS = 1, TQ_ROTATE_VALUES = 2 };
 /* tq_decode / tq_decode_dense flags (reference cache_mlx.py:188-196, 225-232).
- * TQ_F32_PRODUCTS (no reference counterpart) selects the float32 split kernel
- * where the float16-split matrix kernel would run (4-bit rows, groups of 4
- * query heads, head_dim 64 / 128); both accumulate in float32.  tq_decode_scaled
- * always runs the float32 split kernel. */
-enum { TQ_ROTATE_QUERY = 1, TQ_INVERSE_OUTPUT = 2, TQ_F32_PRODUCTS = 4 };
+ * The split kernel (no reference counterpart): the float16-split matrix
+ * kernel can run for 4-bit rows, groups of 4 query heads and head_dim
+ * 64 / 128 / 256, and by default does where its split plan gives every split
+ * at least 4 blocks of 128 rows (8 at head_dim 256); elsewhere the float32
+ * split kernel runs.  Both accumulate in float32.  TQ_F32_PRODUCTS selects
+ * the float32 kernel, TQ_MATRIX_PRODUCTS the matrix kernel wherever it can
+ * run (the two exclude each other: TQ_ERR_BAD_ARG).  tq_decode_scaled always
+ * runs the float32 split kernel. */
+enum { TQ_ROTATE_QUERY = 1, TQ_INVERSE_OUTPUT = 2, TQ_F32_PRODUCTS = 4, TQ_MATRIX_PRODUCTS = 8 };
 
 int tq_abi_version(void);
 const char* tq_last_error(void);
@@ -119,20 +123,22 @@ int tq_unpack_dequantize_scaled(const uint32_t* codes, const float* scales, int6
                                 hipStream_t stream);
 
 /* Split count a decode call over `bits`-bit rows (0 for dense rows) with
- * decode `flags` uses when n_splits <= 0 is passed.  The sequence is dealt
- * out to the splits in blocks of one workgroup iteration (split s takes
- * blocks s, s + n, s + 2n, ...); an explicit n_splits above the number of
- * blocks is lowered to it. */
+ * decode `flags` uses when n_splits <= 0 is passed, on num_cus compute units
+ * (<= 0: the current device's).  The sequence is dealt out to the splits in
+ * blocks of one workgroup iteration (split s takes blocks s, s + n, s + 2n,
+ * ...); an explicit n_splits above the number of blocks is lowered to it. */
 int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int head_dim, int bits, int flags,
                              int64_t seq_len, int num_cus);
 
 /* Name of the split kernel a tq_decode call over `bits`-bit packed rows with
- * decode `flags` and a query of `query_dtype` launches:
- * "decode_mx_kernel<D,QF16>" (the float16-split matrix kernel) or
+ * decode `flags`, a query of `query_dtype`, seq_len tokens and n_splits
+ * (<= 0: the default) launches on num_cus compute units (<= 0: the current
+ * device's): "decode_mx_kernel<D,QF16>" (the float16-split matrix kernel) or
  * "decode_kernel<PackedB<bits>,D,<heads per group>>" (the float32 kernel;
  * tq_decode_scaled always runs this one).  For profiles and benchmarks; no
  * reference counterpart.  NULL on bad arguments (tq_last_error). */
-const char* tq_decode_split_kernel(int kv_heads, int query_heads, int head_dim, int bits, int flags, int query_dtype);
+const char* tq_decode_split_kernel(int num_layers, int kv_heads, int query_heads, int head_dim, int bits, int flags,
+                                   int query_dtype, int64_t seq_len, int n_splits, int num_cus);
 
 /* Bytes of workspace tq_decode / tq_decode_dense need for n_splits splits
  * (n_splits <= 0: enough for the default split count on any sequence length

@@ -45,7 +45,7 @@ def test_host_only_entry_points():
     from torque_hip import _lib
 
     lib = _lib.load()
-    assert lib.tq_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.tq_abi_version() == _lib.ABI_VERSION == 3
     # 4-bit rows in groups of 4 query heads: the f16-split matrix kernel, one 768-thread workgroup per CU
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 32768, 256) == 32
     # the float32-product kernel (requested, or 2-bit rows): two 256-thread workgroups per CU
@@ -54,15 +54,28 @@ def test_host_only_entry_points():
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 7, 256) == 1
     assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, 64, 256) > 64 * 8 * 4 * 128 * 4
     assert lib.tq_decode_workspace_bytes(1, 8, 30, 128, 64, 256) == 0  # Hq not divisible
-    assert _lib.split_kernel(8, 32, 128, 4, 0, _lib.TQ_F16) == "decode_mx_kernel<128,true>"
-    assert _lib.split_kernel(8, 32, 64, 4, 0, _lib.TQ_F32) == "decode_mx_kernel<64,false>"
-    assert _lib.split_kernel(8, 32, 128, 4, _lib.TQ_F32_PRODUCTS, _lib.TQ_F16) == "decode_kernel<PackedB4,128,4>"
-    assert _lib.split_kernel(8, 32, 128, 2, 0, _lib.TQ_F16) == "decode_kernel<PackedB2,128,4>"
-    assert _lib.split_kernel(2, 8, 256, 4, 0, _lib.TQ_F16) == "decode_mx_kernel<256,true>"
-    assert _lib.split_kernel(2, 8, 256, 4, _lib.TQ_F32_PRODUCTS, _lib.TQ_F16) == "decode_kernel<PackedB4,256,4>"
-    assert _lib.split_kernel(4, 8, 128, 4, 0, _lib.TQ_F16) == "decode_kernel<PackedB4,128,2>"
+    mx, f32 = _lib.TQ_MATRIX_PRODUCTS, _lib.TQ_F32_PRODUCTS
+    ks = lambda *a, **k: _lib.split_kernel(*a, num_cus=256, **k)
+    # M: 256 blocks of 128 rows over 32 splits (8 per split): the matrix kernel
+    assert ks(8, 32, 128, 4, 0, _lib.TQ_F16, 32768) == "decode_mx_kernel<128,true>"
+    assert ks(8, 32, 64, 4, 0, _lib.TQ_F32, 32768) == "decode_mx_kernel<64,false>"
+    assert ks(8, 32, 128, 4, f32, _lib.TQ_F16, 32768) == "decode_kernel<PackedB4,128,4>"
+    assert ks(8, 32, 128, 2, 0, _lib.TQ_F16, 32768) == "decode_kernel<PackedB2,128,4>"
+    # head_dim 128 takes the matrix kernel from 4 blocks per split (16K tokens at 8 KV heads), not at 2
+    assert ks(8, 32, 128, 4, 0, _lib.TQ_F16, 16384) == "decode_mx_kernel<128,true>"
+    assert ks(8, 32, 128, 4, 0, _lib.TQ_F16, 8192) == "decode_kernel<PackedB4,128,4>"
+    assert ks(8, 32, 128, 4, 0, _lib.TQ_F16, 8192, n_splits=16) == "decode_mx_kernel<128,true>"
+    # head_dim 256 from 8: C4 (128K tokens, 2 KV heads) yes, a C5 layer (8K tokens, 4 KV heads) no
+    assert ks(2, 8, 256, 4, 0, _lib.TQ_F16, 131072) == "decode_mx_kernel<256,true>"
+    assert ks(2, 8, 256, 4, f32, _lib.TQ_F16, 131072) == "decode_kernel<PackedB4,256,4>"
+    assert ks(4, 16, 256, 4, 0, _lib.TQ_F16, 8192) == "decode_kernel<PackedB4,256,4>"
+    assert ks(4, 16, 256, 4, mx, _lib.TQ_F16, 8192) == "decode_mx_kernel<256,true>"
+    assert ks(4, 16, 256, 4, mx, _lib.TQ_F16, 1, num_layers=24) == "decode_mx_kernel<256,true>"
+    # groups of 2 and 3-bit rows never take it, forced or not
+    assert ks(4, 8, 128, 4, mx, _lib.TQ_F16, 32768) == "decode_kernel<PackedB4,128,2>"
+    assert ks(8, 32, 128, 3, mx, _lib.TQ_F16, 32768) == "decode_kernel<PackedB3,128,4>"
     with pytest.raises(ValueError):
-        _lib.split_kernel(8, 30, 128, 4, 0, _lib.TQ_F16)
+        _lib.split_kernel(8, 30, 128, 4, 0, _lib.TQ_F16, 100)
 
 
 @pytest.mark.parametrize(

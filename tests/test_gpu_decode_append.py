@@ -110,39 +110,47 @@ def test_mixed_kv_dtypes_quantize_at_float32(hip_device):
                                    b.decode(query=q, return_numpy=False).cpu().numpy(), atol=1e-6)
 
 
-def test_decode_append_against_oracle_and_split_counts(hip_device):
+@pytest.mark.parametrize("head_dim", [128, 256])
+def test_decode_append_against_oracle_and_split_counts(hip_device, head_dim):
+    """3000 rows: 1 and 3 splits run the matrix kernel (24 and 8 blocks of 128 rows per split), 64 splits the
+    float32 kernel; every output matches the oracle's append-then-decode."""
     import torque_hip as th
+    from torque_hip import _lib
+
+    D = head_dim
 
     rng = np.random.default_rng(5)
-    cfg = th.TorqueConfig(bit_width=4, head_dim=128, num_layers=1, kv_heads=2)
+    cfg = th.TorqueConfig(bit_width=4, head_dim=D, num_layers=1, kv_heads=2)
     cache = th.TorqueKVCacheHIP(config=cfg, initial_capacity=4096, decode_tail_capacity=0)
-    k0 = rng.normal(size=(1, 2, 3000, 128)).astype(np.float32)
-    v0 = rng.normal(size=(1, 2, 3000, 128)).astype(np.float32)
+    k0 = rng.normal(size=(1, 2, 3000, D)).astype(np.float32)
+    v0 = rng.normal(size=(1, 2, 3000, D)).astype(np.float32)
     cache.append_many(key=k0, value=v0)
-    q = rng.normal(size=(8, 128)).astype(np.float32)
-    kn = rng.normal(size=(2, 128)).astype(np.float32)
-    vn = rng.normal(size=(2, 128)).astype(np.float32)
+    q = rng.normal(size=(8, D)).astype(np.float32)
+    kn = rng.normal(size=(2, D)).astype(np.float32)
+    vn = rng.normal(size=(2, D)).astype(np.float32)
     st = cache._store
+    kernels = [_lib.split_kernel(2, 8, D, 4, 3, _lib.TQ_F32, 3000, n_splits=ns) for ns in (1, 3, 64)]
+    assert kernels[:2] == [f"decode_mx_kernel<{D},false>"] * 2 and kernels[2].startswith("decode_kernel<"), kernels
     outs = []
-    for ns in (1, 5, 64):
+    for ns in (1, 3, 64):
         st.length = 3000  # rewrite the same token at the same row each time
         outs.append(
-            st.decode_append(torch.from_numpy(q).to(hip_device).reshape(1, 8, 128),
-                             torch.from_numpy(kn).to(hip_device).reshape(1, 2, 1, 128),
-                             torch.from_numpy(vn).to(hip_device).reshape(1, 2, 1, 128),
+            st.decode_append(torch.from_numpy(q).to(hip_device).reshape(1, 8, D),
+                             torch.from_numpy(kn).to(hip_device).reshape(1, 2, 1, D),
+                             torch.from_numpy(vn).to(hip_device).reshape(1, 2, 1, D),
                              rotate_query=True, inverse_output=True, rotate_keys=True, rotate_values=True,
                              n_splits=ns).cpu().numpy()[0]
         )
-    model = o.OracleCache(bit_width=4, head_dim=128, num_layers=1, kv_heads=2,
+    model = o.OracleCache(bit_width=4, head_dim=D, num_layers=1, kv_heads=2,
                           key_centroids=cache.key_codebook.centroids, value_centroids=cache.value_codebook.centroids,
                           signs_left=cache.rotation.signs_left, signs_right=cache.rotation.signs_right)
-    model.append(np.concatenate([k0, kn.reshape(1, 2, 1, 128)], axis=2), np.concatenate([v0, vn.reshape(1, 2, 1, 128)], axis=2))
-    exp = model.decode(q.reshape(1, 8, 128))[0]
+    model.append(np.concatenate([k0, kn.reshape(1, 2, 1, D)], axis=2), np.concatenate([v0, vn.reshape(1, 2, 1, D)], axis=2))
+    exp = model.decode(q.reshape(1, 8, D))[0]
     cache.sequence_length = 3001
     kc, vc = _codes(cache)
     np.testing.assert_array_equal(kc.view(np.uint32), model.k_codes)
     np.testing.assert_array_equal(vc.view(np.uint32), model.v_codes)
-    for ns, out in zip((1, 5, 64), outs):
+    for ns, out in zip((1, 3, 64), outs):
         np.testing.assert_allclose(out, exp, atol=2e-6, rtol=1e-5, err_msg=f"n_splits {ns}")
 
 

@@ -59,7 +59,7 @@ def _decode(c, *, layers, kv_heads, group, head_dim, seq_len, capacity, f32_prod
         key_centroids=d["key_centroids"], value_centroids=d["value_centroids"], signs_left=d["signs_left"],
         signs_right=d["signs_right"], rotate_query=rotate, inverse_output=rotate,
         current_keys=None if current is None else current[0], current_values=None if current is None else current[1],
-        n_splits=n_splits, f32_products=f32_products,
+        n_splits=n_splits, f32_products=f32_products, matrix_products=not f32_products,
     ).cpu().numpy()
 
 

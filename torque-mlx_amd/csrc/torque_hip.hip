@@ -1304,10 +1304,36 @@ int decode_block_rows(int fmt, int head_dim) {
   return kTokensPerIter * kWavesPerBlock * kWave * slice_dims / head_dim;
 }
 
-SplitKernel pick_kernel(int fmt, int head_dim, int hg, int flags) {
-  if (fmt == 4 && hg == 4 && (head_dim == 64 || head_dim == 128 || head_dim == 256) && (flags & TQ_F32_PRODUCTS) == 0)
-    return SplitKernel::Mx;
-  return SplitKernel::Fp32;
+// Shapes the matrix-core split kernel takes: 4-bit rows, groups of 4 query
+// heads, head_dim 64 / 128 / 256.
+bool mx_shape(int fmt, int head_dim, int hg) {
+  return fmt == 4 && hg == 4 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+}
+
+// Fewest 128-row blocks per split at which the matrix-core kernel runs by
+// default.  Measured on MI355X (wall time per decode, each kernel on its own
+// default split plan): at head_dim 128 it is level with the float32 kernel at
+// 2 blocks per split and ahead from 4 (0.6 us at 16K tokens x 8 KV heads,
+// 1.6 us at 32K); at head_dim 256 it trails at 1-4 blocks (0.2-1.6 us) and
+// leads at 8 (2.5 us at 64K x 4 and 128K x 2).  With less work per
+// workgroup, writing its 128 KB of tables costs more than its loop saves.
+int mx_min_blocks_per_split(int head_dim) { return head_dim == 256 ? 8 : 4; }
+
+// Split kernel and split count of a decode over `units` work units with
+// decode `flags` (n_splits <= 0: the default count for the chosen kernel).
+struct KernelChoice {
+  SplitKernel kernel;
+  int n_splits;
+};
+KernelChoice choose_kernel(int units, int64_t seq_len, int n_splits, int fmt, int head_dim, int hg, int flags,
+                           int num_cus) {
+  if (mx_shape(fmt, head_dim, hg) && (flags & TQ_F32_PRODUCTS) == 0) {
+    const int ns = n_splits > 0 ? n_splits : default_splits(units, seq_len, num_cus, 1);
+    const int64_t blocks = std::max<int64_t>(1, (seq_len + mx::kStride - 1) / mx::kStride);
+    if ((flags & TQ_MATRIX_PRODUCTS) != 0 || blocks / std::min<int64_t>(blocks, ns) >= mx_min_blocks_per_split(head_dim))
+      return {SplitKernel::Mx, ns};
+  }
+  return {SplitKernel::Fp32, n_splits > 0 ? n_splits : default_splits(units, seq_len, num_cus, 2)};
 }
 
 // Fills the split plan of a decode call over `fmt` rows (see
@@ -1329,10 +1355,12 @@ int make_plan(int num_layers, int kv_heads, int query_heads, int64_t seq_len, in
   if (units > max_wg)
     return fail(TQ_ERR_BAD_ARG, "num_layers x kv_heads x head groups exceeds one launch; decode fewer layers per call");
   p->units = static_cast<int>(units);
-  p->kernel = pick_kernel(fmt, head_dim, p->hg, flags);
+  if ((flags & TQ_F32_PRODUCTS) != 0 && (flags & TQ_MATRIX_PRODUCTS) != 0)
+    return fail(TQ_ERR_BAD_ARG, "TQ_F32_PRODUCTS and TQ_MATRIX_PRODUCTS exclude each other");
+  const KernelChoice kc = choose_kernel(p->units, seq_len, n_splits, fmt, head_dim, p->hg, flags, device_cu_count());
+  p->kernel = kc.kernel;
   p->block_rows = p->kernel == SplitKernel::Mx ? mx::kStride : decode_block_rows(fmt, head_dim);
-  const int wgs_per_cu = p->kernel == SplitKernel::Mx ? 1 : 2;
-  int ns = n_splits > 0 ? n_splits : default_splits(p->units, seq_len, device_cu_count(), wgs_per_cu);
+  const int ns = kc.n_splits;
   if (ns > kMaxSplits) return fail(TQ_ERR_BAD_ARG, "n_splits must be at most " + std::to_string(kMaxSplits));
   const int64_t blocks = std::max<int64_t>(1, (seq_len + p->block_rows - 1) / p->block_rows);
   p->n_splits = static_cast<int>(std::min<int64_t>({blocks, static_cast<int64_t>(ns), max_wg / units}));
@@ -2085,13 +2113,14 @@ int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int 
   const int group = query_heads / kv_heads;
   const int hg = pick_hg(group);
   const int units = num_layers * kv_heads * (group / hg);
-  const bool mx_kernel = pick_kernel(bits, head_dim, hg, flags) == SplitKernel::Mx;
-  return default_splits(units, seq_len, num_cus, mx_kernel ? 1 : 2);
+  if (num_cus <= 0) num_cus = device_cu_count();
+  return choose_kernel(units, seq_len, 0, bits, head_dim, hg, flags, num_cus).n_splits;
 }
 
-const char* tq_decode_split_kernel(int kv_heads, int query_heads, int head_dim, int bits, int flags,
-                                   int query_dtype) {
-  if (kv_heads <= 0 || query_heads <= 0 || query_heads % kv_heads != 0 || !valid_head_dim(head_dim)) {
+const char* tq_decode_split_kernel(int num_layers, int kv_heads, int query_heads, int head_dim, int bits, int flags,
+                                   int query_dtype, int64_t seq_len, int n_splits, int num_cus) {
+  if (num_layers <= 0 || kv_heads <= 0 || query_heads <= 0 || query_heads % kv_heads != 0 ||
+      !valid_head_dim(head_dim) || seq_len < 0) {
     fail(TQ_ERR_BAD_ARG, "bad head configuration");
     return nullptr;
   }
@@ -2100,9 +2129,12 @@ const char* tq_decode_split_kernel(int kv_heads, int query_heads, int head_dim, 
     fail(TQ_ERR_UNSUPPORTED, "split kernel names cover packed rows (bits 2, 3, 4)");
     return nullptr;
   }
-  const int hg = pick_hg(query_heads / kv_heads);
+  const int group = query_heads / kv_heads;
+  const int hg = pick_hg(group);
+  const int units = num_layers * kv_heads * (group / hg);
+  if (num_cus <= 0) num_cus = device_cu_count();
   static thread_local std::string name;
-  if (pick_kernel(bits, head_dim, hg, flags) == SplitKernel::Mx)
+  if (choose_kernel(units, seq_len, n_splits, bits, head_dim, hg, flags, num_cus).kernel == SplitKernel::Mx)
     name = "decode_mx_kernel<" + std::to_string(head_dim) + "," + (query_dtype == TQ_F16 ? "true" : "false") + ">";
   else
     name = "decode_kernel<PackedB" + std::to_string(bits) + "," + std::to_string(head_dim) + "," +

@@ -19,7 +19,7 @@ import torch  # noqa: F401  -- load torch's HIP runtime first
 LIB_NAME = "libtorque_hip.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TQ_OK = 0
 TQ_ERR_BAD_ARG = -1
@@ -34,6 +34,7 @@ TQ_ROTATE_VALUES = 2
 TQ_ROTATE_QUERY = 1
 TQ_INVERSE_OUTPUT = 2
 TQ_F32_PRODUCTS = 4
+TQ_MATRIX_PRODUCTS = 8
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -54,7 +55,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tq_unpack_dequantize": (_i, [_p, _i64, _i64, _i64, _i, _i, _p, _p, _p]),
     "tq_unpack_dequantize_scaled": (_i, [_p, _p, _i64, _i64, _i64, _i, _i, _p, _p, _p]),
     "tq_decode_default_splits": (_i, [_i, _i, _i, _i, _i, _i, _i64, _i]),
-    "tq_decode_split_kernel": (ctypes.c_char_p, [_i, _i, _i, _i, _i, _i]),
+    "tq_decode_split_kernel": (ctypes.c_char_p, [_i, _i, _i, _i, _i, _i, _i, _i64, _i, _i]),
     "tq_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "tq_decode": (
         _i,
@@ -149,9 +150,12 @@ def call(name: str, *args) -> int:
     return rc
 
 
-def split_kernel(kv_heads: int, query_heads: int, head_dim: int, bits: int, flags: int, query_dtype: int) -> str:
-    """Name of the split kernel tq_decode launches for this shape and flags (tq_decode_split_kernel)."""
-    name = load().tq_decode_split_kernel(kv_heads, query_heads, head_dim, bits, flags, query_dtype)
+def split_kernel(kv_heads: int, query_heads: int, head_dim: int, bits: int, flags: int, query_dtype: int,
+                 seq_len: int, num_layers: int = 1, n_splits: int = 0, num_cus: int = 0) -> str:
+    """Name of the split kernel tq_decode launches for this call shape (tq_decode_split_kernel; n_splits 0
+    is the default plan, num_cus 0 the current device's compute units)."""
+    name = load().tq_decode_split_kernel(num_layers, kv_heads, query_heads, head_dim, bits, flags, query_dtype,
+                                         seq_len, n_splits, num_cus)
     if name is None:
         raise ValueError(load().tq_last_error().decode("utf-8", "replace"))
     return name.decode()

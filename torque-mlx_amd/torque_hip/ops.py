@@ -116,6 +116,7 @@ def packed_decode(
     key_scales: torch.Tensor | None = None,
     value_scales: torch.Tensor | None = None,
     f32_products: bool = False,
+    matrix_products: bool = False,
 ) -> torch.Tensor:
     """One ``tq_decode`` launch on device tensors; returns out[L, Hq, D] float32.
 
@@ -124,11 +125,14 @@ def packed_decode(
     ``f32_products`` selects the float32-product split kernel (TQ_F32_PRODUCTS)
     where the float16-split matrix kernel would run; scaled decodes always
     take it (the library adds the flag), so their split plan does too.
+    ``matrix_products`` (TQ_MATRIX_PRODUCTS) runs the matrix kernel wherever it
+    can, also where the default plan leaves too few rows per split for it.
     """
     dev = query.device
     scaled = key_scales is not None or value_scales is not None
     flags = (_lib.TQ_ROTATE_QUERY if rotate_query else 0) | (_lib.TQ_INVERSE_OUTPUT if inverse_output else 0)
     flags |= _lib.TQ_F32_PRODUCTS if f32_products or scaled else 0
+    flags |= _lib.TQ_MATRIX_PRODUCTS if matrix_products else 0
     if n_splits is None or n_splits <= 0:
         n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev, bit_width=bit_width,
                                flags=flags)
