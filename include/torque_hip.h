@@ -43,10 +43,10 @@ enum { TQ_F32 = 0, TQ_F16 = 1 };
 enum { TQ_ROTATE_KEYS = 1, TQ_ROTATE_VALUES = 2 };
 /* tq_decode / tq_decode_dense flags (reference cache_mlx.py:188-196, 225-232).
  * The split kernel (no reference counterpart): the float16-split matrix
- * kernel can run for 4-bit rows, groups of 4 query heads and head_dim
- * 64 / 128 / 256, and by default does where its split plan gives every split
- * at least 4 blocks of 128 rows (8 at head_dim 256); elsewhere the float32
- * split kernel runs.  Both accumulate in float32.  TQ_F32_PRODUCTS selects
+ * kernel can run for groups of 4 query heads with 4-bit rows at head_dim
+ * 64 / 128 / 256 or 2-bit rows at head_dim 128, and by default does where
+ * its split plan gives every split at least 4 blocks of 128 rows (8 at
+ * head_dim 256); elsewhere the float32 split kernel runs.  Both accumulate in float32.  TQ_F32_PRODUCTS selects
  * the float32 kernel, TQ_MATRIX_PRODUCTS the matrix kernel wherever it can
  * run (the two exclude each other: TQ_ERR_BAD_ARG).  tq_decode_scaled always
  * runs the float32 split kernel. */
@@ -133,7 +133,8 @@ int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int 
 /* Name of the split kernel a tq_decode call over `bits`-bit packed rows with
  * decode `flags`, a query of `query_dtype`, seq_len tokens and n_splits
  * (<= 0: the default) launches on num_cus compute units (<= 0: the current
- * device's): "decode_mx_kernel<D,QF16>" (the float16-split matrix kernel) or
+ * device's): "decode_mx_kernel<D,QF16>" (the float16-split matrix kernel;
+ * "decode_mx_kernel<D,QF16,2>" for 2-bit rows) or
  * "decode_kernel<PackedB<bits>,D,<heads per group>>" (the float32 kernel;
  * tq_decode_scaled always runs this one).  For profiles and benchmarks; no
  * reference counterpart.  NULL on bad arguments (tq_last_error). */

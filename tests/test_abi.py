@@ -48,9 +48,10 @@ def test_host_only_entry_points():
     assert lib.tq_abi_version() == _lib.ABI_VERSION == 3
     # 4-bit rows in groups of 4 query heads: the f16-split matrix kernel, one 768-thread workgroup per CU
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 32768, 256) == 32
-    # the float32-product kernel (requested, or 2-bit rows): two 256-thread workgroups per CU
+    # the float32-product kernel (requested, or 3-bit rows): two 256-thread workgroups per CU
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 4, 32768, 256) == 64
-    assert lib.tq_decode_default_splits(1, 8, 32, 128, 2, 0, 32768, 256) == 64
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 2, 0, 32768, 256) == 32  # 2-bit: the matrix kernel too
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 3, 0, 32768, 256) == 64
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 7, 256) == 1
     assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, 64, 256) > 64 * 8 * 4 * 128 * 4
     assert lib.tq_decode_workspace_bytes(1, 8, 30, 128, 64, 256) == 0  # Hq not divisible
@@ -60,7 +61,9 @@ def test_host_only_entry_points():
     assert ks(8, 32, 128, 4, 0, _lib.TQ_F16, 32768) == "decode_mx_kernel<128,true>"
     assert ks(8, 32, 64, 4, 0, _lib.TQ_F32, 32768) == "decode_mx_kernel<64,false>"
     assert ks(8, 32, 128, 4, f32, _lib.TQ_F16, 32768) == "decode_kernel<PackedB4,128,4>"
-    assert ks(8, 32, 128, 2, 0, _lib.TQ_F16, 32768) == "decode_kernel<PackedB2,128,4>"
+    assert ks(8, 32, 128, 2, 0, _lib.TQ_F16, 32768) == "decode_mx_kernel<128,true,2>"
+    assert ks(8, 32, 128, 2, f32, _lib.TQ_F16, 32768) == "decode_kernel<PackedB2,128,4>"
+    assert ks(8, 32, 64, 2, mx, _lib.TQ_F16, 32768) == "decode_kernel<PackedB2,64,4>"
     # head_dim 128 takes the matrix kernel from 4 blocks per split (16K tokens at 8 KV heads), not at 2
     assert ks(8, 32, 128, 4, 0, _lib.TQ_F16, 16384) == "decode_mx_kernel<128,true>"
     assert ks(8, 32, 128, 4, 0, _lib.TQ_F16, 8192) == "decode_kernel<PackedB4,128,4>"

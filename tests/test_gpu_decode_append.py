@@ -110,8 +110,8 @@ def test_mixed_kv_dtypes_quantize_at_float32(hip_device):
                                    b.decode(query=q, return_numpy=False).cpu().numpy(), atol=1e-6)
 
 
-@pytest.mark.parametrize("head_dim", [128, 256])
-def test_decode_append_against_oracle_and_split_counts(hip_device, head_dim):
+@pytest.mark.parametrize("bits,head_dim", [(4, 128), (4, 256), (2, 128)])
+def test_decode_append_against_oracle_and_split_counts(hip_device, bits, head_dim):
     """3000 rows: 1 and 3 splits run the matrix kernel (24 and 8 blocks of 128 rows per split), 64 splits the
     float32 kernel; every output matches the oracle's append-then-decode."""
     import torque_hip as th
@@ -120,7 +120,7 @@ def test_decode_append_against_oracle_and_split_counts(hip_device, head_dim):
     D = head_dim
 
     rng = np.random.default_rng(5)
-    cfg = th.TorqueConfig(bit_width=4, head_dim=D, num_layers=1, kv_heads=2)
+    cfg = th.TorqueConfig(bit_width=bits, head_dim=D, num_layers=1, kv_heads=2)
     cache = th.TorqueKVCacheHIP(config=cfg, initial_capacity=4096, decode_tail_capacity=0)
     k0 = rng.normal(size=(1, 2, 3000, D)).astype(np.float32)
     v0 = rng.normal(size=(1, 2, 3000, D)).astype(np.float32)
@@ -129,8 +129,9 @@ def test_decode_append_against_oracle_and_split_counts(hip_device, head_dim):
     kn = rng.normal(size=(2, D)).astype(np.float32)
     vn = rng.normal(size=(2, D)).astype(np.float32)
     st = cache._store
-    kernels = [_lib.split_kernel(2, 8, D, 4, 3, _lib.TQ_F32, 3000, n_splits=ns) for ns in (1, 3, 64)]
-    assert kernels[:2] == [f"decode_mx_kernel<{D},false>"] * 2 and kernels[2].startswith("decode_kernel<"), kernels
+    kernels = [_lib.split_kernel(2, 8, D, bits, 3, _lib.TQ_F32, 3000, n_splits=ns) for ns in (1, 3, 64)]
+    mx_name = f"decode_mx_kernel<{D},false>" if bits == 4 else f"decode_mx_kernel<{D},false,{bits}>"
+    assert kernels[:2] == [mx_name] * 2 and kernels[2].startswith("decode_kernel<"), kernels
     outs = []
     for ns in (1, 3, 64):
         st.length = 3000  # rewrite the same token at the same row each time
@@ -141,7 +142,7 @@ def test_decode_append_against_oracle_and_split_counts(hip_device, head_dim):
                              rotate_query=True, inverse_output=True, rotate_keys=True, rotate_values=True,
                              n_splits=ns).cpu().numpy()[0]
         )
-    model = o.OracleCache(bit_width=4, head_dim=D, num_layers=1, kv_heads=2,
+    model = o.OracleCache(bit_width=bits, head_dim=D, num_layers=1, kv_heads=2,
                           key_centroids=cache.key_codebook.centroids, value_centroids=cache.value_codebook.centroids,
                           signs_left=cache.rotation.signs_left, signs_right=cache.rotation.signs_right)
     model.append(np.concatenate([k0, kn.reshape(1, 2, 1, D)], axis=2), np.concatenate([v0, vn.reshape(1, 2, 1, D)], axis=2))

@@ -141,6 +141,9 @@ __device__ __forceinline__ uint32_t lut_addr_dyn(uint32_t w, uint32_t base, int 
 __device__ __forceinline__ uint2 lds_read_u2(const uint8_t* smem, uint32_t addr) {
   return *reinterpret_cast<const uint2*>(smem + addr);
 }
+__device__ __forceinline__ uint4 lds_read_u4(const uint8_t* smem, uint32_t addr) {
+  return *reinterpret_cast<const uint4*>(smem + addr);
+}
 
 __device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -185,15 +188,61 @@ __device__ __forceinline__ void write_tables(uint8_t* smem, float cvec, int sh_k
   }
 }
 
+// 2-bit tables: entry e (one code byte: four codes c_r = (e >> 2r) & 3) is
+// 16 bytes, replicated 16 times (copy c at e * 256 + c * 16, so a lane's
+// 16-byte read of copy lane % 16 is conflict-free whatever the codes).  Key
+// entry: (hi c_0, hi c_1), (lo c_0, lo c_1), (hi c_2, hi c_3), (lo c_2, lo c_3)
+// -- four dims of one token, the k-slot order of one score product.  Value
+// entry: (hi c_r, lo c_r) for r = 0..3 -- one dim of four tokens.  Span and
+// entry numbering as in write_tables (e = 4 (s % 64) + l / 16): c_0 =
+// c[l / 16] is fixed per lane, c_1 = c[s % 4], c_2 = c[(s / 4) % 4], c_3 =
+// c[(s / 16) % 4] are uniform over the span.  cvec: lane j < 16 holds key
+// centroid j % 4, lane 16 + j value centroid j % 4.
+template <int W>
+__device__ __forceinline__ void write_tables2(uint8_t* smem, float cvec, int sh_k, int sh_v, int w, int lane) {
+  constexpr int kSpans = 2 * kTableBytes / 1024;
+  constexpr int kPer = kSpans / W;
+  static_assert(kSpans % W == 0 && kPer % 2 == 0, "spans split evenly, keys then values");
+  const int g = lane >> 4;
+  const float c0k = __shfl(cvec, g), c0v = __shfl(cvec, 16 + g);
+  const int cbits = __builtin_bit_cast(int, cvec);
+  auto split = [](float c, int sh, _Float16& hi, _Float16& lo) {
+    const float x = ldexpf(c, sh);
+    hi = static_cast<_Float16>(x);
+    lo = static_cast<_Float16>(x - static_cast<float>(hi));
+  };
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int span = w + W * k;
+    const bool key = k < kPer / 2;
+    const int tb = key ? 0 : 16;
+    const int sh = key ? sh_k : sh_v;
+    const float c[4] = {key ? c0k : c0v,
+                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(cbits, tb + (span & 3))),
+                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(cbits, tb + ((span >> 2) & 3))),
+                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(cbits, tb + ((span >> 4) & 3)))};
+    _Float16 hi[4], lo[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) split(c[r], sh, hi[r], lo[r]);
+    const uint4 e = key ? make_uint4(pack_f16x2(hi[0], hi[1]), pack_f16x2(lo[0], lo[1]), pack_f16x2(hi[2], hi[3]),
+                                     pack_f16x2(lo[2], lo[3]))
+                        : make_uint4(pack_f16x2(hi[0], lo[0]), pack_f16x2(hi[1], lo[1]), pack_f16x2(hi[2], lo[2]),
+                                     pack_f16x2(hi[3], lo[3]));
+    *reinterpret_cast<uint4*>(smem + (span << 10) + (lane << 4)) = e;
+  }
+}
+
 }  // namespace mx
 
-template <int D, bool QF16>
+template <int D, bool QF16, int BITS = 4>
 __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
     amdgpu_waves_per_eu(mx::waves_of<D>() / 4, mx::waves_of<D>() / 4))) void decode_mx_kernel(
     const DecodeArgs a) {
   using namespace mx;
   static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128 or 256");
-  constexpr int ROW = D / 2;          // packed bytes per row (4-bit)
+  static_assert(BITS == 4 || (BITS == 2 && D == 128), "4-bit rows, or 2-bit rows at head_dim 128");
+  constexpr bool B2 = BITS == 2;      // 2-bit rows: 16-byte table entries, one per code byte
+  constexpr int ROW = D * BITS / 8;   // packed bytes per row
   constexpr int KB = ROW / 4;         // key bytes per lane per tile (a quarter row)
   constexpr int KW = (KB + 3) / 4;    // key dwords per lane (KB = 8, 16, 32)
   constexpr int NS = D / 16;          // score products per tile
@@ -251,7 +300,8 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   // Per-lane load offsets inside a tile: key quarter g of row n; value dword
   // n (and 16 + n at D = 256; dword n / 2 at D = 64) of rows 4g + r.
   const int koff = n * ROW + g * KB;
-  const int voff = (4 * g) * ROW + 4 * (D == 64 ? (n >> 1) : n);
+  constexpr int RW = ROW / 4;  // dwords per row
+  const int voff = (4 * g) * ROW + 4 * (RW >= 16 ? n : (n >> 1));
   struct Raw {
     uint32_t k[KW];
     uint32_t v[4][VW];
@@ -285,11 +335,12 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   // the first tiles' rows: vector loads return in order, so a set-up value
   // requested after the rows would wait for them.
   // centroids in lanes: lane j < 16 key centroid j, lane 16 + j value centroid j
-  const float* cptr = lane < 16 ? a.cent_k + lane : a.cent_v + (lane & 15);
+  constexpr int NC = 1 << BITS;  // centroids per table
+  const float* cptr = lane < 16 ? a.cent_k + (lane & (NC - 1)) : a.cent_v + (lane & (NC - 1));
   const float cvec = lane < 32 ? *cptr : 0.f;
   const bool appending = a.new_k != nullptr;
   const bool appender = appending && split == 0 && wave < 2;
-  constexpr int kLevels = 15;
+  constexpr int kLevels = NC - 1;
   float tok[E], bnd[kLevels];
   if (appender) {
     const int64_t toff = static_cast<int64_t>(lkv) * D + lane * E;
@@ -339,7 +390,12 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   // power-of-two scales of the two tables (lane rows 0 and 1 hold their centroids)
   const int sh_lane = scale_shift(group_reduce<16, OpMax>(fabsf(cvec)));
   const int sh_k = __builtin_amdgcn_readlane(sh_lane, 0), sh_v = __builtin_amdgcn_readlane(sh_lane, 16);
-  if (wave >= 4) write_tables<NW - 4>(smem, cvec, sh_k, sh_v, wave - 4, lane);
+  if (wave >= 4) {
+    if constexpr (B2)
+      write_tables2<NW - 4>(smem, cvec, sh_k, sh_v, wave - 4, lane);
+    else
+      write_tables<NW - 4>(smem, cvec, sh_k, sh_v, wave - 4, lane);
+  }
   if (wave == 4 && lane == 0) s_misc[4] = ldexpf(1.f, -(sh_v + 7));  // weights carry 2^7, values 2^sh_v
 
   // ---- append mode: rotate (as on append) and quantize the new token.
@@ -347,7 +403,7 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
     if (wave == 1 ? a.rotate_new_v : a.rotate_new_k) wave_rotate_signs<D>(tok, sg_first, sg_second, a.sqrt_d);
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      const uint32_t code = quantize_count<4>(tok[i], bnd);
+      const uint32_t code = quantize_count<BITS>(tok[i], bnd);
       s_codes[wave * D + lane * E + i] = static_cast<uint8_t>(code);
       s_cur[wave * D + lane * E + i] = (wave == 0 ? a.cent_k : a.cent_v)[code];
     }
@@ -386,10 +442,10 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   // prefetched rows in flight
   lds_barrier();
   if (appender) {
-    constexpr int W = D * 4 / 32;
+    constexpr int W = D * BITS / 32;
     if (hg == 0 && lane < W) {
       uint32_t* dst = (wave == 0 ? a.k_slab : a.v_slab) + (static_cast<int64_t>(lkv) * a.cap + a.seq_len) * W + lane;
-      *dst = pack_word<4, D>(s_codes + wave * D, lane);
+      *dst = pack_word<BITS, D>(s_codes + wave * D, lane);
     }
   }
 
@@ -403,9 +459,10 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   const float score_scale = s_misc[n & 3];
   const float out_scale = s_misc[4];
 
-  // table bases (offsets into smem): copy lane % 32, key table at 0, value
+  // table bases (offsets into smem): copy lane % 32 of 8-byte entries
+  // (4-bit) or lane % 16 of 16-byte entries (2-bit), key table at 0, value
   // table at 65536; bits 8..15 stay clear for the code byte
-  const uint32_t base_k = (lane & 31) * 8;
+  const uint32_t base_k = B2 ? (lane & 15) * 16 : (lane & 31) * 8;
   const uint32_t base_v = base_k + kTableBytes;
 
   // Softmax state, log2 units.  Lane m works on head m % 4: m_lane is that
@@ -430,16 +487,49 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   //   score products(i + 1)
   // (the key reads have the softmax and value products to land, the value
   // reads the score products and the next iteration's first half).
-  uint2 kl[KBH];      // key lookups of one half, one per byte of the lane's quarter row
-  uint2 vl[NVH][2];   // value lookups of one half: product j, token pair (0, 1) / (2, 3)
+  using KeyL = std::conditional_t<B2, uint4, uint2>;
+  KeyL kl[KBH];       // key lookups of one half, one per byte of the lane's quarter row
+  uint2 vl[NVH][2];   // 4-bit value lookups of one half: product j, token pair (0, 1) / (2, 3)
+  uint4 vl4[B2 ? NVH : 1];  // 2-bit value lookups: product j, tokens 0..3
   auto key_lookups = [&](const Raw& r, int h) {
 #pragma unroll
-    for (int b = 0; b < KBH; ++b) kl[b] = lds_read_u2(smem, lut_addr_dyn(r.k[(h * KBH + b) / 4], base_k, b & 3));
+    for (int b = 0; b < KBH; ++b) {
+      const uint32_t addr = lut_addr_dyn(r.k[(h * KBH + b) / 4], base_k, b & 3);
+      if constexpr (B2)
+        kl[b] = lds_read_u4(smem, addr);
+      else
+        kl[b] = lds_read_u2(smem, addr);
+    }
+  };
+  // 2-bit values: lane (n, g) takes dims 8n .. 8n + 7 -- fields 8 (n & 1) + j
+  // of dword n / 2 of rows 4g .. 4g + 3.  The fields of one dim in the four
+  // rows are gathered into one byte (row r at bits 2r), the lookup key of the
+  // value table; the four words below hold those bytes for all 16 fields of
+  // the dword (field f in word f % 4, byte f / 4), and the lane's selectors
+  // pick byte 2 (n & 1) (j < 4) or 2 (n & 1) + 1 (j >= 4).
+  const uint32_t vsel0 = 0x03020000u | ((4u + 2u * (n & 1)) << 8);
+  const uint32_t vsel1 = vsel0 + 0x100u;
+  auto value_lookups2 = [&](const Raw& r) {
+    const uint32_t h0 = r.v[0][0], h1 = r.v[1][0], h2 = r.v[2][0], h3 = r.v[3][0];
+    // nibble k of P (Q): field 2k (2k + 1) of rows 0 and 1; P2, Q2 rows 2 and 3
+    const uint32_t P = (h0 & 0x33333333u) | ((h1 << 2) & 0xccccccccu);
+    const uint32_t Q = ((h0 >> 2) & 0x33333333u) | (h1 & 0xccccccccu);
+    const uint32_t P2 = (h2 & 0x33333333u) | ((h3 << 2) & 0xccccccccu);
+    const uint32_t Q2 = ((h2 >> 2) & 0x33333333u) | (h3 & 0xccccccccu);
+    const uint32_t F[4] = {(P & 0x0f0f0f0fu) | ((P2 << 4) & 0xf0f0f0f0u),     // fields 0, 4, 8, 12
+                           (Q & 0x0f0f0f0fu) | ((Q2 << 4) & 0xf0f0f0f0u),     // fields 1, 5, 9, 13
+                           ((P >> 4) & 0x0f0f0f0fu) | (P2 & 0xf0f0f0f0u),     // fields 2, 6, 10, 14
+                           ((Q >> 4) & 0x0f0f0f0fu) | (Q2 & 0xf0f0f0f0u)};    // fields 3, 7, 11, 15
+#pragma unroll
+    for (int j = 0; j < NVH; ++j)
+      vl4[j] = lds_read_u4(smem, __builtin_amdgcn_perm(F[j & 3], base_v, j < 4 ? vsel0 : vsel1));
   };
   // value dword q = h of the lane's rows (dims 128 h + 8 n .. + 7; D = 64:
   // the n & 1 half of dword n / 2)
   auto value_lookups = [&](const Raw& r, int h) {
-    {
+    if constexpr (B2) {
+      value_lookups2(r);
+    } else {
       const int q = h;
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) {
@@ -463,7 +553,11 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
 #pragma unroll
     for (int s2 = 0; s2 < NSH; ++s2) {
       const int q2 = 2 * (h * NSH + s2);
-      const f16x8 A = as_f16x8(kl[2 * s2].x, kl[2 * s2].y, kl[2 * s2 + 1].x, kl[2 * s2 + 1].y);
+      f16x8 A;
+      if constexpr (B2)
+        A = __builtin_bit_cast(f16x8, kl[s2]);
+      else
+        A = as_f16x8(kl[2 * s2].x, kl[2 * s2].y, kl[2 * s2 + 1].x, kl[2 * s2 + 1].y);
       const f16x8 B = as_f16x8(qd[q2], qd[q2], qd[q2 + 1], qd[q2 + 1]);
       ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, ds, 0, 0, 0);
     }
@@ -532,7 +626,11 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   auto value_products = [&](const f16x8& Aw, int h) {
 #pragma unroll
     for (int j = 0; j < NVH; ++j) {
-      const f16x8 B = as_f16x8(vl[j][0].x, vl[j][0].y, vl[j][1].x, vl[j][1].y);
+      f16x8 B;
+      if constexpr (B2)
+        B = __builtin_bit_cast(f16x8, vl4[j]);
+      else
+        B = as_f16x8(vl[j][0].x, vl[j][0].y, vl[j][1].x, vl[j][1].y);
       acc[h * NVH + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aw, B, acc[h * NVH + j], 0, 0, 0);
     }
   };

@@ -1304,10 +1304,11 @@ int decode_block_rows(int fmt, int head_dim) {
   return kTokensPerIter * kWavesPerBlock * kWave * slice_dims / head_dim;
 }
 
-// Shapes the matrix-core split kernel takes: 4-bit rows, groups of 4 query
-// heads, head_dim 64 / 128 / 256.
+// Shapes the matrix-core split kernel takes: groups of 4 query heads with
+// 4-bit rows at head_dim 64 / 128 / 256 or 2-bit rows at head_dim 128.
 bool mx_shape(int fmt, int head_dim, int hg) {
-  return fmt == 4 && hg == 4 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+  return hg == 4 && ((fmt == 4 && (head_dim == 64 || head_dim == 128 || head_dim == 256)) ||
+                     (fmt == 2 && head_dim == 128));
 }
 
 // Fewest 128-row blocks per split at which the matrix-core kernel runs by
@@ -1443,38 +1444,44 @@ int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hi
 int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream,
                  bool profiled);
 
-template <int D, bool QF16>
+template <int D, bool QF16, int BITS>
 void launch_mx_t(const DecodeArgs& a, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (start != nullptr || stop != nullptr)
-    hipExtLaunchKernelGGL((decode_mx_kernel<D, QF16>), grid, dim3(mx::threads_of<D>()), 0, stream, start, stop, 0, a);
+    hipExtLaunchKernelGGL((decode_mx_kernel<D, QF16, BITS>), grid, dim3(mx::threads_of<D>()), 0, stream, start,
+                          stop, 0, a);
   else
-    hipLaunchKernelGGL((decode_mx_kernel<D, QF16>), grid, dim3(mx::threads_of<D>()), 0, stream, a);
+    hipLaunchKernelGGL((decode_mx_kernel<D, QF16, BITS>), grid, dim3(mx::threads_of<D>()), 0, stream, a);
 }
 
-template <int D>
+template <int D, int BITS>
 void launch_mx_d(const DecodeArgs& a, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (a.q_f16)
-    launch_mx_t<D, true>(a, grid, stream, start, stop);
+    launch_mx_t<D, true, BITS>(a, grid, stream, start, stop);
   else
-    launch_mx_t<D, false>(a, grid, stream, start, stop);
+    launch_mx_t<D, false, BITS>(a, grid, stream, start, stop);
 }
 
 // Grid (split, head group, layer x KV head) of decode_mx_kernel.
-int launch_mx(const DecodeArgs& a, int head_dim, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+int launch_mx(const DecodeArgs& a, int fmt, int head_dim, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   constexpr int kMaxGridYZ = 65535;
   const int lkv = a.num_layers * a.kv_heads;
   if (lkv > kMaxGridYZ || a.n_hgroups > kMaxGridYZ)
     return fail(TQ_ERR_BAD_ARG, "num_layers x kv_heads must be at most 65535 per call; decode fewer layers per call");
   const dim3 grid(a.n_splits, a.n_hgroups, lkv);
+  if (fmt == 2 && head_dim == 128) {
+    launch_mx_d<128, 2>(a, grid, stream, start, stop);
+    return TQ_OK;
+  }
+  if (fmt != 4) return fail(TQ_ERR_UNSUPPORTED, "decode_mx_kernel: unsupported bit width " + std::to_string(fmt));
   switch (head_dim) {
     case 64:
-      launch_mx_d<64>(a, grid, stream, start, stop);
+      launch_mx_d<64, 4>(a, grid, stream, start, stop);
       return TQ_OK;
     case 128:
-      launch_mx_d<128>(a, grid, stream, start, stop);
+      launch_mx_d<128, 4>(a, grid, stream, start, stop);
       return TQ_OK;
     case 256:
-      launch_mx_d<256>(a, grid, stream, start, stop);
+      launch_mx_d<256, 4>(a, grid, stream, start, stop);
       return TQ_OK;
     default:
       return fail(TQ_ERR_UNSUPPORTED, "decode_mx_kernel: unsupported head dimension " + std::to_string(head_dim));
@@ -1589,7 +1596,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   m.out = out;
 
   if (p.kernel == SplitKernel::Mx) {
-    rc = launch_mx(a, head_dim, stream, start, stop);
+    rc = launch_mx(a, fmt, head_dim, stream, start, stop);
   } else {
     rc = launch_fp32(a, fmt, head_dim, p.hg, nblk, stream, start, stop);
   }
@@ -2135,7 +2142,8 @@ const char* tq_decode_split_kernel(int num_layers, int kv_heads, int query_heads
   if (num_cus <= 0) num_cus = device_cu_count();
   static thread_local std::string name;
   if (choose_kernel(units, seq_len, n_splits, bits, head_dim, hg, flags, num_cus).kernel == SplitKernel::Mx)
-    name = "decode_mx_kernel<" + std::to_string(head_dim) + "," + (query_dtype == TQ_F16 ? "true" : "false") + ">";
+    name = "decode_mx_kernel<" + std::to_string(head_dim) + "," + (query_dtype == TQ_F16 ? "true" : "false") +
+           (bits == 4 ? ">" : "," + std::to_string(bits) + ">");
   else
     name = "decode_kernel<PackedB" + std::to_string(bits) + "," + std::to_string(head_dim) + "," +
            std::to_string(hg) + ">";
