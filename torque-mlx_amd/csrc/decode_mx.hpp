@@ -154,13 +154,19 @@ __device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, ui
 // ce1 = c[e >> 4], scaled by 2^sh: key table (hi(ce0), hi(ce1)),
 // (lo(ce0), lo(ce1)) (two dims of one token), value table (hi(ce0),
 // lo(ce0)), (hi(ce1), lo(ce1)) (one dim of two tokens).
-__device__ __forceinline__ uint2 table_entry(float ce0, float ce1, int sh, bool key) {
-  const float c0 = ldexpf(ce0, sh), c1 = ldexpf(ce1, sh);
-  const _Float16 h0 = static_cast<_Float16>(c0), h1 = static_cast<_Float16>(c1);
-  const _Float16 l0 = static_cast<_Float16>(c0 - static_cast<float>(h0));
-  const _Float16 l1 = static_cast<_Float16>(c1 - static_cast<float>(h1));
-  return key ? make_uint2(pack_f16x2(h0, h1), pack_f16x2(l0, l1)) : make_uint2(pack_f16x2(h0, l0), pack_f16x2(h1, l1));
+// The split of one centroid scaled by 2^sh: hi = f16(c 2^sh) in the low half,
+// lo = f16(c 2^sh - hi) in the high half.  Lane j of a writer computes the
+// split of the centroid it holds; table entries are then byte permutations of
+// two or four such words.
+__device__ __forceinline__ uint32_t centroid_split(float c, int sh) {
+  const float x = ldexpf(c, sh);
+  const _Float16 hi = static_cast<_Float16>(x);
+  const _Float16 lo = static_cast<_Float16>(x - static_cast<float>(hi));
+  return pack_f16x2(hi, lo);
 }
+// (hi a, hi b) and (lo a, lo b) from the splits a, b: the key table's k-slot pairs.
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
 // Writes both tables from the centroids: writer wavefront w (0..W-1, W = 8
 // or 4) fills the 1 KB spans w, w + W, ..., w + 128 - W; in span s lane l
@@ -176,14 +182,15 @@ __device__ __forceinline__ void write_tables(uint8_t* smem, float cvec, int sh_k
   constexpr int kPer = kSpans / W;
   static_assert(W % 4 == 0 && kSpans % W == 0 && kPer % 2 == 0, "spans split evenly, keys then values");
   const int src0 = 4 * (w & 3) + (lane >> 4);
-  const float c0k = __shfl(cvec, src0), c0v = __shfl(cvec, 16 + src0);
-  const int cbits = __builtin_bit_cast(int, cvec);
+  const int split = static_cast<int>(centroid_split(cvec, lane < 16 ? sh_k : sh_v));
+  const uint32_t p0k = __shfl(split, src0), p0v = __shfl(split, 16 + src0);
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int span = w + W * k;
     const bool key = k < kPer / 2;
-    const float c1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(cbits, (key ? 0 : 16) + ((span >> 2) & 15)));
-    const uint2 e = table_entry(key ? c0k : c0v, c1, key ? sh_k : sh_v, key);
+    const uint32_t p1 = __builtin_amdgcn_readlane(split, (key ? 0 : 16) + ((span >> 2) & 15));
+    // key entry (hi c0, hi c1), (lo c0, lo c1); value entry (hi c0, lo c0), (hi c1, lo c1)
+    const uint2 e = key ? make_uint2(hi_pair(p0k, p1), lo_pair(p0k, p1)) : make_uint2(p0v, p1);
     *reinterpret_cast<uint4*>(smem + (span << 10) + (lane << 4)) = make_uint4(e.x, e.y, e.x, e.y);
   }
 }
@@ -204,30 +211,18 @@ __device__ __forceinline__ void write_tables2(uint8_t* smem, float cvec, int sh_
   constexpr int kPer = kSpans / W;
   static_assert(kSpans % W == 0 && kPer % 2 == 0, "spans split evenly, keys then values");
   const int g = lane >> 4;
-  const float c0k = __shfl(cvec, g), c0v = __shfl(cvec, 16 + g);
-  const int cbits = __builtin_bit_cast(int, cvec);
-  auto split = [](float c, int sh, _Float16& hi, _Float16& lo) {
-    const float x = ldexpf(c, sh);
-    hi = static_cast<_Float16>(x);
-    lo = static_cast<_Float16>(x - static_cast<float>(hi));
-  };
+  const int split = static_cast<int>(centroid_split(cvec, lane < 16 ? sh_k : sh_v));
+  const uint32_t p0k = __shfl(split, g), p0v = __shfl(split, 16 + g);
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int span = w + W * k;
     const bool key = k < kPer / 2;
     const int tb = key ? 0 : 16;
-    const int sh = key ? sh_k : sh_v;
-    const float c[4] = {key ? c0k : c0v,
-                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(cbits, tb + (span & 3))),
-                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(cbits, tb + ((span >> 2) & 3))),
-                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(cbits, tb + ((span >> 4) & 3)))};
-    _Float16 hi[4], lo[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) split(c[r], sh, hi[r], lo[r]);
-    const uint4 e = key ? make_uint4(pack_f16x2(hi[0], hi[1]), pack_f16x2(lo[0], lo[1]), pack_f16x2(hi[2], hi[3]),
-                                     pack_f16x2(lo[2], lo[3]))
-                        : make_uint4(pack_f16x2(hi[0], lo[0]), pack_f16x2(hi[1], lo[1]), pack_f16x2(hi[2], lo[2]),
-                                     pack_f16x2(hi[3], lo[3]));
+    const uint32_t p[4] = {key ? p0k : p0v, static_cast<uint32_t>(__builtin_amdgcn_readlane(split, tb + (span & 3))),
+                           static_cast<uint32_t>(__builtin_amdgcn_readlane(split, tb + ((span >> 2) & 3))),
+                           static_cast<uint32_t>(__builtin_amdgcn_readlane(split, tb + ((span >> 4) & 3)))};
+    const uint4 e = key ? make_uint4(hi_pair(p[0], p[1]), lo_pair(p[0], p[1]), hi_pair(p[2], p[3]), lo_pair(p[2], p[3]))
+                        : make_uint4(p[0], p[1], p[2], p[3]);
     *reinterpret_cast<uint4*>(smem + (span << 10) + (lane << 4)) = e;
   }
 }
