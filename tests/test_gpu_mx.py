@@ -159,6 +159,32 @@ def test_matrix_kernel_rotation_and_current_token(hip_device, head_dim, bits):
             np.testing.assert_allclose(mx, f32, rtol=2e-5, atol=2e-6 * np.abs(f32).max(), err_msg=f"{ns} {current is None}")
 
 
+@pytest.mark.parametrize("head_dim,bits", [(128, 4), (256, 4), (128, 2)])
+def test_matrix_kernel_empty_sequence(hip_device, head_dim, bits):
+    """No rows, the matrix kernel forced: zeros without a current token (the reference's S = 0 case,
+    cache_mlx.py:178-180), the current token's value alone with one (its softmax weight is 1) -- the
+    same outputs as the float32 kernel, on one split and on several empty ones."""
+    geo = dict(layers=1, kv_heads=2, group=4, head_dim=head_dim, seq_len=0, bits=bits)
+    c = _case(17, capacity=8, q_dtype=torch.float32, q_scale=1.0, dev=hip_device, **geo)
+    gen = torch.Generator(device=hip_device).manual_seed(4)
+    cur = (torch.randn((1, 2, head_dim), generator=gen, device=hip_device),
+           torch.randn((1, 2, head_dim), generator=gen, device=hip_device))
+    for ns in (None, 1, 3):
+        for current in (None, cur):
+            mx = _decode(c, capacity=8, f32_products=False, n_splits=ns, rotate=True, current=current, **geo)
+            f32 = _decode(c, capacity=8, f32_products=True, n_splits=ns, rotate=True, current=current, **geo)
+            assert np.isfinite(mx).all(), (ns, current is None)
+            if current is None:
+                assert not mx.any() and not f32.any(), ns
+            else:
+                np.testing.assert_allclose(mx, f32, rtol=1e-6, atol=1e-6, err_msg=f"{ns}")
+                # the current token's value (given in the rotated basis) rotated back, for every
+                # query head of its KV head
+                signs_l, signs_r = c["np"]["signs"]
+                expect = o.rotation_inverse(np.repeat(current[1].cpu().numpy()[0], 4, axis=0), signs_l, signs_r)
+                np.testing.assert_allclose(mx[0], expect, rtol=1e-5, atol=1e-5, err_msg=f"{ns}")
+
+
 def test_matrix_kernel_repeatable_across_calls(hip_device):
     """Tiles are claimed dynamically, so the summation order may change between calls: outputs
     stay within float32 rounding of each other and never pick up stale state."""
