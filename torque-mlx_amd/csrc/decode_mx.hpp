@@ -96,14 +96,20 @@ struct Smem {
   static constexpr int kCurBytes = 2 * D * 4 + 2 * D;  // append mode: s_cur [2][D] + codes [2][D]
   static constexpr int kMisc = 1024;
   static constexpr int kNW = waves_of<D>();
-  static constexpr int kRS = D <= 128 ? D + 10 : D + 18;       // padded reduction row (floats)
-  static constexpr int kRedBytes = kNW * 4 * kRS * 4;           // after the loop, inside the table area
+  static constexpr int kRS = D == 128 ? D + 6 : D < 128 ? D + 10 : D + 18;  // padded reduction row (floats)
+  static constexpr int kRedBytes = kNW * 4 * kRS * 4 + 2 * kNW * 4 * 4;      // rows, then (max, sum) per wave
   static constexpr int kQb = 2 * kTableBytes;
   static constexpr int kQ = kQb + kQbBytes;
   static constexpr int kCur = kQ + kQBytes;
   static constexpr int kMiscOff = kCur + kCurBytes;
-  static constexpr int kTotal = kMiscOff + kMisc;
-  static_assert(kRedBytes + 2 * kNW * 4 * 4 <= 2 * kTableBytes, "reduction fits in the table area");
+  static constexpr int kSetup = kMiscOff + kMisc;
+  // The reduction sits beside the tables where the LDS holds both (head_dim
+  // 64 and 128), so each wavefront deposits its partial as soon as its own
+  // loop ends; at head_dim 256 it reuses the table area after a barrier.
+  static constexpr bool kRedApart = kSetup + kRedBytes <= 160 * 1024;
+  static constexpr int kRed = kRedApart ? kSetup : 0;
+  static constexpr int kTotal = kRedApart ? kSetup + kRedBytes : kSetup;
+  static_assert(kRedApart || kRedBytes <= 2 * kTableBytes, "reduction fits in the table area");
 };
 
 __device__ __forceinline__ uint32_t pack_f16x2(_Float16 lo, _Float16 hi) {
@@ -666,13 +672,13 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
 
   // ---- combine: rows h and 4 + h (lane groups 0 and 1), then the
   // wavefronts.  Lane n of group 0 holds head rr's output at dims of column n.
-  __syncthreads();  // the tables are dead: reuse their space
+  if constexpr (!L::kRedApart) __syncthreads();  // the tables are dead: reuse their space
   // s_red: [NW x 4 heads] rows of RS floats; dim d of a row sits at
   // d + 4 (d / 64), and RS = 2 (mod 4) and above that, so that the 32 lanes writing one
   // register pair (16 dims x 2 rows) hit 32 distinct banks
   constexpr int RS = L::kRS;
-  float* s_red = reinterpret_cast<float*>(smem);
-  float* s_mw = reinterpret_cast<float*>(smem + NW * 4 * RS * 4);  // [NW][4]
+  float* s_red = reinterpret_cast<float*>(smem + L::kRed);
+  float* s_mw = reinterpret_cast<float*>(smem + L::kRed + NW * 4 * RS * 4);  // [NW][4]
   float* s_lw = s_mw + NW * 4;                                       // [NW][4]
   auto red_pos = [](int d) { return d + 4 * (d >> 6); };
 #pragma unroll
@@ -695,7 +701,7 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
       s_lw[wave * 4 + lane] = lw;
     }
   }
-  __syncthreads();
+  lds_barrier();  // the wavefronts' partials meet in LDS
 
   auto wave_weights = [&](int h, float (&f)[NW]) {
     float M = s_mw[h];
