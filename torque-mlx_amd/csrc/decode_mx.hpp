@@ -188,13 +188,13 @@ __device__ __forceinline__ void write_tables(uint8_t* smem, float cvec, int sh_k
   constexpr int kPer = kSpans / W;
   static_assert(W % 4 == 0 && kSpans % W == 0 && kPer % 2 == 0, "spans split evenly, keys then values");
   const int src0 = 4 * (w & 3) + (lane >> 4);
-  const int split = static_cast<int>(centroid_split(cvec, lane < 16 ? sh_k : sh_v));
-  const uint32_t p0k = __shfl(split, src0), p0v = __shfl(split, 16 + src0);
+  const int pair = static_cast<int>(centroid_split(cvec, lane < 16 ? sh_k : sh_v));
+  const uint32_t p0k = __shfl(pair, src0), p0v = __shfl(pair, 16 + src0);
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int span = w + W * k;
     const bool key = k < kPer / 2;
-    const uint32_t p1 = __builtin_amdgcn_readlane(split, (key ? 0 : 16) + ((span >> 2) & 15));
+    const uint32_t p1 = __builtin_amdgcn_readlane(pair, (key ? 0 : 16) + ((span >> 2) & 15));
     // key entry (hi c0, hi c1), (lo c0, lo c1); value entry (hi c0, lo c0), (hi c1, lo c1)
     const uint2 e = key ? make_uint2(hi_pair(p0k, p1), lo_pair(p0k, p1)) : make_uint2(p0v, p1);
     *reinterpret_cast<uint4*>(smem + (span << 10) + (lane << 4)) = make_uint4(e.x, e.y, e.x, e.y);
@@ -217,16 +217,16 @@ __device__ __forceinline__ void write_tables2(uint8_t* smem, float cvec, int sh_
   constexpr int kPer = kSpans / W;
   static_assert(kSpans % W == 0 && kPer % 2 == 0, "spans split evenly, keys then values");
   const int g = lane >> 4;
-  const int split = static_cast<int>(centroid_split(cvec, lane < 16 ? sh_k : sh_v));
-  const uint32_t p0k = __shfl(split, g), p0v = __shfl(split, 16 + g);
+  const int pair = static_cast<int>(centroid_split(cvec, lane < 16 ? sh_k : sh_v));
+  const uint32_t p0k = __shfl(pair, g), p0v = __shfl(pair, 16 + g);
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int span = w + W * k;
     const bool key = k < kPer / 2;
     const int tb = key ? 0 : 16;
-    const uint32_t p[4] = {key ? p0k : p0v, static_cast<uint32_t>(__builtin_amdgcn_readlane(split, tb + (span & 3))),
-                           static_cast<uint32_t>(__builtin_amdgcn_readlane(split, tb + ((span >> 2) & 3))),
-                           static_cast<uint32_t>(__builtin_amdgcn_readlane(split, tb + ((span >> 4) & 3)))};
+    const uint32_t p[4] = {key ? p0k : p0v, static_cast<uint32_t>(__builtin_amdgcn_readlane(pair, tb + (span & 3))),
+                           static_cast<uint32_t>(__builtin_amdgcn_readlane(pair, tb + ((span >> 2) & 3))),
+                           static_cast<uint32_t>(__builtin_amdgcn_readlane(pair, tb + ((span >> 4) & 3)))};
     const uint4 e = key ? make_uint4(hi_pair(p[0], p[1]), lo_pair(p[0], p[1]), hi_pair(p[2], p[3]), lo_pair(p[2], p[3]))
                         : make_uint4(p[0], p[1], p[2], p[3]);
     *reinterpret_cast<uint4*>(smem + (span << 10) + (lane << 4)) = e;
