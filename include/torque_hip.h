@@ -2,8 +2,10 @@
  * torque_hip.h -- C ABI of the MI355X (gfx950) packed rotated KV-cache decode path.
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t.
- * The library allocates nothing and keeps no device state; the caller owns
- * all buffers (slabs, centroids, signs, workspaces, outputs).  Kernels are
+ * The library allocates nothing; the caller owns all buffers (slabs,
+ * centroids, signs, workspaces, outputs).  Its only device state is the fixed
+ * per-GPU scratch array of tq_decode_noalloc, the entry point for callers that
+ * cannot allocate a workspace.  Kernels are
  * launched asynchronously on `stream`.  Return value: TQ_OK (0) or a negative
  * TQ_ERR_* code; tq_last_error() gives the message (thread-local).
  *
