@@ -103,6 +103,37 @@ def test_decode_argument_errors(args, code, message):
     assert message in lib.tq_last_error().decode()
 
 
+def test_last_error_is_per_thread():
+    """tq_last_error() is thread-local: two threads that fail differently at the same moment each read
+    back their own message (validation runs on the host before any launch, so no GPU is needed)."""
+    import threading
+
+    from torque_hip import _lib
+
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    barrier = threading.Barrier(2, timeout=30)  # a thread that dies breaks it instead of hanging the other
+    seen: dict[int, list[str]] = {96: [], 5: []}
+
+    def run(head_dim, bits, key):
+        for _ in range(50):
+            rc = lib.tq_decode(fake, 0, 1, 32, 8, head_dim, bits, fake, fake, 10, 10, fake, fake, None, None, 0,
+                               None, None, 0, fake, 1 << 30, fake, None)
+            assert rc == -2
+            barrier.wait()  # both threads have set their error before either reads it
+            seen[key].append(lib.tq_last_error().decode())
+            barrier.wait()
+
+    threads = [threading.Thread(target=run, args=(96, 4, 96)), threading.Thread(target=run, args=(128, 5, 5))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert len(seen[96]) == len(seen[5]) == 50
+    assert all("Unsupported head dimension: 96" in m for m in seen[96])
+    assert all("Unsupported bit width: 5" in m for m in seen[5])
+
+
 @pytest.mark.parametrize(
     ("num_layers", "seq_len", "n_splits", "message"),
     [

@@ -1,0 +1,53 @@
+"""Concurrent decodes on two streams.
+
+The kernels keep no state between calls and every call brings its own
+workspace, so decodes issued on two streams at once return what they return
+one after another: bit for bit on the float32-product kernel (its work split
+is static), to float32 rounding on the matrix kernel (its wavefronts claim
+tiles dynamically, so the summation order may change).  The reference runs on
+one MLX stream (cache_mlx.py); the boundary here promises stateless,
+stream-ordered launches, and this is that promise under overlap.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(dev, seed, kv_heads, seq_len, head_dim=128, bits=4, group=4):
+    rng = np.random.default_rng(seed)
+    words = head_dim * bits // 32
+    codes = lambda: torch.from_numpy(
+        rng.integers(0, 2**32, size=(1, kv_heads, seq_len, words), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    ).to(dev)
+    cent = lambda s: torch.from_numpy((np.sort(rng.normal(size=1 << bits)) * s).astype(np.float32)).to(dev)
+    q = torch.from_numpy(rng.normal(size=(1, kv_heads * group, head_dim)).astype(np.float32)).to(dev, torch.float16)
+    return dict(query=q, key_codes=codes(), value_codes=codes(), key_centroids=cent(1.5), value_centroids=cent(0.1),
+                num_layers=1, query_heads=kv_heads * group, kv_heads=kv_heads, head_dim=head_dim, bit_width=bits,
+                capacity=seq_len, seq_len=seq_len)
+
+
+@pytest.mark.parametrize("f32_products", [True, False])
+def test_two_streams_match_sequential(hip_device, f32_products):
+    from torque_hip.ops import packed_decode
+
+    cases = [_inputs(hip_device, 1, kv_heads=8, seq_len=16384), _inputs(hip_device, 2, kv_heads=4, seq_len=20000)]
+    decode = lambda c: packed_decode(**c, f32_products=f32_products, matrix_products=not f32_products)
+    ref = [decode(c).cpu().numpy() for c in cases]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(hip_device), torch.cuda.Stream(hip_device)
+    for rep in range(3):
+        with torch.cuda.stream(s1):
+            a = decode(cases[0])
+        with torch.cuda.stream(s2):
+            b = decode(cases[1])
+        torch.cuda.synchronize()
+        for got, exp in zip((a.cpu().numpy(), b.cpu().numpy()), ref):
+            if f32_products:
+                np.testing.assert_array_equal(got, exp, err_msg=f"rep {rep}")
+            else:
+                np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-6 * np.abs(exp).max(), err_msg=f"rep {rep}")
