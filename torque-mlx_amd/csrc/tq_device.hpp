@@ -258,8 +258,16 @@ __device__ __forceinline__ void wave_rotate_signs(float (&v)[D / kWave], const f
 #pragma unroll
   for (int i = 0; i < E; ++i) v[i] = __fmul_rn(v[i], s_first[i]);
   wave_fwht<D>(v);
+  if constexpr (D == 64 || D == 256) {
+    // sqrt(D) is a power of two (sqrt_d = 8 or 16 exactly): multiplying by
+    // its exact reciprocal rounds like the division, denormals included
+    constexpr float kInv = D == 64 ? 0.125f : 0.0625f;
 #pragma unroll
-  for (int i = 0; i < E; ++i) v[i] = __fmul_rn(__fdiv_rn(v[i], sqrt_d), s_second[i]);
+    for (int i = 0; i < E; ++i) v[i] = __fmul_rn(__fmul_rn(v[i], kInv), s_second[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = __fmul_rn(__fdiv_rn(v[i], sqrt_d), s_second[i]);
+  }
 }
 template <int D>
 __device__ __forceinline__ void wave_rotate(float (&v)[D / kWave], const float* __restrict__ s_first,
