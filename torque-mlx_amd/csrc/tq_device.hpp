@@ -221,6 +221,24 @@ __device__ __forceinline__ void fwht_cross(float (&v)[E], int lane) {
   }
 }
 
+// The stages 16 and 32 apart on two of a lane's elements at once: after one
+// permlane swap of (a, b) the lower lane of each pair holds (a_lower,
+// a_upper) and the upper lane (b_lower, b_upper), so one add and one subtract
+// form both butterflies (left + right, left - right, left the lower lane, as
+// in fwht_cross), and a second swap of (sum, difference) returns new a and
+// new b to their lanes.  Same operations on the same operands: bit-identical.
+template <int M, int E>
+__device__ __forceinline__ void fwht_cross_pairs(float (&v)[E]) {
+  static_assert(E % 2 == 0, "pairs of elements");
+#pragma unroll
+  for (int i = 0; i < E; i += 2) {
+    const LanePair p = permlane_swap<M>(v[i], v[i + 1]);
+    const LanePair q = permlane_swap<M>(__fadd_rn(p.first, p.second), __fsub_rn(p.first, p.second));
+    v[i] = q.first;
+    v[i + 1] = q.second;
+  }
+}
+
 template <int D>
 __device__ __forceinline__ void wave_fwht(float (&v)[D / kWave]) {
   constexpr int E = D / kWave;
@@ -240,8 +258,13 @@ __device__ __forceinline__ void wave_fwht(float (&v)[D / kWave]) {
   fwht_cross<2>(v, lane);
   fwht_cross<4>(v, lane);
   fwht_cross<8>(v, lane);
-  fwht_cross<16>(v, lane);
-  fwht_cross<32>(v, lane);
+  if constexpr (E >= 2) {
+    fwht_cross_pairs<16>(v);
+    fwht_cross_pairs<32>(v);
+  } else {
+    fwht_cross<16>(v, lane);
+    fwht_cross<32>(v, lane);
+  }
 }
 
 // y = s_second * (H (s_first * x)) / sqrt(D), with the reference's operation
