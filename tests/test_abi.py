@@ -53,6 +53,12 @@ def test_host_only_entry_points():
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 2, 0, 32768, 256) == 32  # 2-bit: the matrix kernel too
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 3, 0, 32768, 256) == 64
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 7, 256) == 1
+    # a length cap just above one workgroup per CU drops to one per CU: 8192 + t tokens over 4 KV heads
+    # would take 65 splits (260 workgroups), 8192 + 4096 tokens 96 (384, far enough over to keep)
+    assert lib.tq_decode_default_splits(1, 4, 16, 256, 4, 0, 8192, 256) == 64
+    assert lib.tq_decode_default_splits(1, 4, 16, 256, 4, 0, 8193, 256) == 64
+    assert lib.tq_decode_default_splits(1, 4, 16, 256, 4, 0, 8192 + 4096, 256) == 96
+    assert lib.tq_decode_default_splits(1, 8, 8, 64, 3, 0, 4096 + 64, 256) == 32  # 33 x 8 = 264 workgroups
     assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, 64, 256) > 64 * 8 * 4 * 128 * 4
     assert lib.tq_decode_workspace_bytes(1, 8, 30, 128, 64, 256) == 0  # Hq not divisible
     mx, f32 = _lib.TQ_MATRIX_PRODUCTS, _lib.TQ_F32_PRODUCTS
