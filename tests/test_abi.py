@@ -80,6 +80,15 @@ def test_host_only_entry_points():
     assert ks(4, 16, 256, 4, 0, _lib.TQ_F16, 8192) == "decode_kernel<PackedB4,256,4>"
     assert ks(4, 16, 256, 4, mx, _lib.TQ_F16, 8192) == "decode_mx_kernel<256,true>"
     assert ks(4, 16, 256, 4, mx, _lib.TQ_F16, 1, num_layers=24) == "decode_mx_kernel<256,true>"
+    # 3 tokens per lane group (48-row iterations) where the 32-row deal leaves a nearly empty last iteration:
+    # 8193..9216 rows over 64 splits (5 narrow against 3 wide), not 8192 (4 against 3), 9217 (73 splits: 4
+    # against 3) or long sequences (forced float32 kernel at C4: 16 against 11)
+    assert ks(4, 16, 256, 4, 0, _lib.TQ_F16, 8193) == "decode_kernel<PackedB4,256,4,3>"
+    assert ks(4, 16, 256, 4, 0, _lib.TQ_F16, 9216) == "decode_kernel<PackedB4,256,4,3>"
+    assert ks(4, 16, 256, 4, 0, _lib.TQ_F16, 9217) == "decode_kernel<PackedB4,256,4>"
+    assert ks(4, 16, 256, 4, 0, _lib.TQ_F16, 8192) == "decode_kernel<PackedB4,256,4>"
+    assert ks(4, 8, 256, 4, 0, _lib.TQ_F16, 8193) == "decode_kernel<PackedB4,256,2>"  # groups of 2: no such instance
+    assert ks(4, 16, 256, 2, 0, _lib.TQ_F16, 8193) == "decode_kernel<PackedB2,256,4>"
     # groups of 2 and 3-bit rows never take it, forced or not
     assert ks(4, 8, 128, 4, mx, _lib.TQ_F16, 32768) == "decode_kernel<PackedB4,128,2>"
     assert ks(8, 32, 128, 3, mx, _lib.TQ_F16, 32768) == "decode_kernel<PackedB3,128,4>"

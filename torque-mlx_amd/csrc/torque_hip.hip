@@ -74,6 +74,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;
 constexpr int kMaxSplits = 256;
 constexpr int kTokensPerIter = 2;  // tokens per lane group per loop iteration
+constexpr int kWideTokensPerIter = 3;  // the same, in the instances of wide_iter_shape
 constexpr int kPrefetchIters = 1;  // loop iterations whose loads are in flight ahead
 constexpr int kScoreChains = 2;    // independent score product chains per token (matrix-core mode)
 constexpr bool kPhaseFences = true;  // matrix-core mode: no interleaving of products with VALU work
@@ -229,6 +230,7 @@ struct DecodeArgs {
   // scale.
   const float* k_scales;
   const float* v_scales;
+  int wide_iter;  // host side only: launch the kWideTokensPerIter instance
 };
 
 // Finish one output row held by a wavefront: optional extra dense token
@@ -312,13 +314,12 @@ __device__ __forceinline__ float slice_sum_select(f32x4 c, int lane) {
   return v;
 }
 
-template <class Fmt, int D, int HG, bool QF16, bool SCALED>
+template <class Fmt, int D, int HG, bool QF16, bool SCALED, int U = kTokensPerIter>
 __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   constexpr int SD = Fmt::kSliceDims;
   constexpr int LPT = D / SD;        // lanes per token
   constexpr int TPW = kWave / LPT;   // tokens (lane groups) per wavefront
   constexpr int TPB = kWavesPerBlock * TPW;
-  constexpr int U = kTokensPerIter;
   constexpr int PF = kPrefetchIters;
   constexpr int NB = PF + 1;         // ring of iteration slots
   constexpr int STRIDE = U * TPB;    // tokens per workgroup iteration
@@ -1219,6 +1220,7 @@ struct Plan {
   int hg, n_hgroups, units, n_splits;
   SplitKernel kernel;
   int block_rows;  // rows per workgroup iteration (the unit the sequence is dealt out in)
+  int tokens_per_iter;  // decode_kernel: tokens per lane group per iteration
 };
 
 constexpr int kMinTokensPerSplit = 128;
@@ -1314,10 +1316,38 @@ void* device_scratch() {
 // bits, 16 dense fp16, 32 dense fp32): tokens per lane group x lane groups
 // per wavefront (64 / (D / slice dims)) x wavefronts; packed slices hold 16
 // dimensions, fp16 rows 8, fp32 rows 4.
-int decode_block_rows(int fmt, int head_dim) {
+int decode_block_rows(int fmt, int head_dim, int tokens_per_iter = kTokensPerIter) {
   const bool packed = fmt == 2 || fmt == 3 || fmt == 4;
   const int slice_dims = packed ? 16 : (fmt == 16 ? 8 : 4);
-  return kTokensPerIter * kWavesPerBlock * kWave * slice_dims / head_dim;
+  return tokens_per_iter * kWavesPerBlock * kWave * slice_dims / head_dim;
+}
+
+// decode_kernel also has instances with kWideTokensPerIter tokens per lane
+// group for 4-bit rows at head_dim 256 in groups of 4 query heads (48 rows
+// per workgroup iteration against 32; 211 VGPRs, no spills).
+template <class Fmt, int D, int HG>
+constexpr bool wide_iter_instance() {
+  return std::is_same_v<Fmt, PackedB4> && D == 256 && HG == 4;
+}
+bool wide_iter_shape(int fmt, int head_dim, int hg) { return fmt == 4 && head_dim == 256 && hg == 4; }
+
+// Tokens per lane group per iteration of a decode_kernel call over seq_len
+// rows and at most `ns_cap` splits.  Two measurements on MI355X (4 KV heads,
+// 64 splits) put a wide iteration at about 1.6 narrow ones: at 8193-8320
+// rows (5 iterations of 32 rows on the longest split against 3 of 48) a
+// 24-layer decode loop takes 275 against 289 us per step, at 8192 rows (4
+// against 3) one layer 11.2 against 10.0 us.  So the wide instance runs
+// where 1.6 x its iterations stay below the narrow count: where the last
+// narrow iteration is a nearly empty one, not on long sequences.
+int fp32_tokens_per_iter(int fmt, int head_dim, int hg, int64_t seq_len, int64_t ns_cap) {
+  if (!wide_iter_shape(fmt, head_dim, hg)) return kTokensPerIter;
+  auto iters = [&](int u) {
+    const int64_t rows = decode_block_rows(fmt, head_dim, u);
+    const int64_t blocks = std::max<int64_t>(1, (seq_len + rows - 1) / rows);
+    const int64_t ns = std::max<int64_t>(1, std::min(blocks, ns_cap));
+    return (blocks + ns - 1) / ns;
+  };
+  return 8 * iters(kWideTokensPerIter) < 5 * iters(kTokensPerIter) ? kWideTokensPerIter : kTokensPerIter;
 }
 
 // Shapes the matrix-core split kernel takes: groups of 4 query heads with
@@ -1376,21 +1406,32 @@ int make_plan(int num_layers, int kv_heads, int query_heads, int64_t seq_len, in
     return fail(TQ_ERR_BAD_ARG, "TQ_F32_PRODUCTS and TQ_MATRIX_PRODUCTS exclude each other");
   const KernelChoice kc = choose_kernel(p->units, seq_len, n_splits, fmt, head_dim, p->hg, flags, device_cu_count());
   p->kernel = kc.kernel;
-  p->block_rows = p->kernel == SplitKernel::Mx ? mx::kStride : decode_block_rows(fmt, head_dim);
   const int ns = kc.n_splits;
   if (ns > kMaxSplits) return fail(TQ_ERR_BAD_ARG, "n_splits must be at most " + std::to_string(kMaxSplits));
+  p->tokens_per_iter = p->kernel == SplitKernel::Mx
+                           ? 0
+                           : fp32_tokens_per_iter(fmt, head_dim, p->hg, seq_len, std::min<int64_t>(ns, max_wg / units));
+  p->block_rows = p->kernel == SplitKernel::Mx ? mx::kStride : decode_block_rows(fmt, head_dim, p->tokens_per_iter);
   const int64_t blocks = std::max<int64_t>(1, (seq_len + p->block_rows - 1) / p->block_rows);
   p->n_splits = static_cast<int>(std::min<int64_t>({blocks, static_cast<int64_t>(ns), max_wg / units}));
   return TQ_OK;
 }
 
+template <class Fmt, int D, int HG, bool QF16, bool SC, int U>
+void launch_decode_u(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  if (start != nullptr || stop != nullptr)
+    hipExtLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16, SC, U>), dim3(nblk), dim3(kBlock), 0, stream, start, stop,
+                          0, a);
+  else
+    hipLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16, SC, U>), dim3(nblk), dim3(kBlock), 0, stream, a);
+}
+
 template <class Fmt, int D, int HG, bool QF16, bool SC>
 void launch_decode_q(const DecodeArgs& a, int nblk, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
-  if (start != nullptr || stop != nullptr)
-    hipExtLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16, SC>), dim3(nblk), dim3(kBlock), 0, stream, start, stop, 0,
-                          a);
-  else
-    hipLaunchKernelGGL((decode_kernel<Fmt, D, HG, QF16, SC>), dim3(nblk), dim3(kBlock), 0, stream, a);
+  if constexpr (wide_iter_instance<Fmt, D, HG>()) {
+    if (a.wide_iter) return launch_decode_u<Fmt, D, HG, QF16, SC, kWideTokensPerIter>(a, nblk, stream, start, stop);
+  }
+  launch_decode_u<Fmt, D, HG, QF16, SC, kTokensPerIter>(a, nblk, stream, start, stop);
 }
 
 // Scaled kernels exist for packed rows only (the host never passes scales
@@ -1594,6 +1635,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
     a.rotate_new_v = (app->flags & TQ_ROTATE_VALUES) != 0;
   }
   a.n_splits = p.n_splits;
+  a.wide_iter = p.tokens_per_iter == kWideTokensPerIter;
   a.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
   a.ws_acc = reinterpret_cast<float*>(ws + wl.acc);
   a.ws_cur_s = reinterpret_cast<float*>(ws + wl.cur_s);
@@ -2157,9 +2199,12 @@ const char* tq_decode_split_kernel(int num_layers, int kv_heads, int query_heads
   const int units = num_layers * kv_heads * (group / hg);
   if (num_cus <= 0) num_cus = device_cu_count();
   static thread_local std::string name;
-  if (choose_kernel(units, seq_len, n_splits, bits, head_dim, hg, flags, num_cus).kernel == SplitKernel::Mx)
+  const KernelChoice kc = choose_kernel(units, seq_len, n_splits, bits, head_dim, hg, flags, num_cus);
+  if (kc.kernel == SplitKernel::Mx)
     name = "decode_mx_kernel<" + std::to_string(head_dim) + "," + (query_dtype == TQ_F16 ? "true" : "false") +
            (bits == 4 ? ">" : "," + std::to_string(bits) + ">");
+  else if (fp32_tokens_per_iter(bits, head_dim, hg, seq_len, kc.n_splits) == kWideTokensPerIter)
+    name = "decode_kernel<PackedB4,256,4," + std::to_string(kWideTokensPerIter) + ">";
   else
     name = "decode_kernel<PackedB" + std::to_string(bits) + "," + std::to_string(head_dim) + "," +
            std::to_string(hg) + ">";
