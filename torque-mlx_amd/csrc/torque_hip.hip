@@ -314,6 +314,8 @@ __device__ __forceinline__ float slice_sum_select(f32x4 c, int lane) {
   return v;
 }
 
+// U: tokens per lane group per loop iteration -- kTokensPerIter, or
+// kWideTokensPerIter in the instances wide_iter_instance() names.
 template <class Fmt, int D, int HG, bool QF16, bool SCALED, int U = kTokensPerIter>
 __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   constexpr int SD = Fmt::kSliceDims;
