@@ -4,8 +4,8 @@
 
 A step is one decode of one query token per query head over the whole packed
 cache: query rotation, split-K packed attention with online softmax,
-cross-workgroup log-sum-exp merge and inverse rotation -- one kernel launch
-(tq_decode).  Inputs (packed K/V slabs) are resident in HBM before timing; the
+cross-workgroup log-sum-exp merge and inverse rotation -- one tq_decode call
+(the split kernel, then the merge kernel).  Inputs (packed K/V slabs) are resident in HBM before timing; the
 timed loop cycles through enough slab replicas (> 512 MiB together) that the
 256 MB Infinity Cache cannot hold the working set.
 
