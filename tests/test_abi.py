@@ -59,6 +59,11 @@ def test_host_only_entry_points():
     assert lib.tq_decode_default_splits(1, 4, 16, 256, 4, 0, 8193, 256) == 64
     assert lib.tq_decode_default_splits(1, 4, 16, 256, 4, 0, 8192 + 4096, 256) == 96
     assert lib.tq_decode_default_splits(1, 8, 8, 64, 3, 0, 4096 + 64, 256) == 32  # 33 x 8 = 264 workgroups
+    # head-group counts that do not divide the target round down, so no workgroup runs in a second wave:
+    # 3 x 85 = 255 (matrix kernel, one per CU) and 3 x 170 = 510 (float32 kernel, two per CU)
+    assert lib.tq_decode_default_splits(1, 3, 12, 128, 4, 0, 1 << 16, 256) == 85
+    assert lib.tq_decode_default_splits(1, 3, 12, 128, 4, 4, 1 << 16, 256) == 170
+    assert lib.tq_decode_default_splits(1, 5, 20, 128, 3, 0, 1 << 16, 256) == 102
     assert lib.tq_decode_workspace_bytes(1, 8, 32, 128, 64, 256) > 64 * 8 * 4 * 128 * 4
     assert lib.tq_decode_workspace_bytes(1, 8, 30, 128, 64, 256) == 0  # Hq not divisible
     mx, f32 = _lib.TQ_MATRIX_PRODUCTS, _lib.TQ_F32_PRODUCTS
