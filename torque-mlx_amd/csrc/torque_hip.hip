@@ -344,11 +344,16 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
 
   // ---- work item.  Consecutive workgroup ids land on different XCDs
   // (round robin over 8); remap so the splits of one head group are
-  // dispatched to the same XCD and share its L2.
+  // dispatched to the same XCD and share its L2.  XCD x receives the ids
+  // x, x + 8, ...: nblk / 8 of them, one more for x < nblk % 8, and takes
+  // that many consecutive work items starting at x (nblk / 8) + min(x,
+  // nblk % 8), so every work item is taken exactly once for any nblk
+  // (3 head groups x 170 splits: float32-kernel median 12.4-12.6 ->
+  // 12.0-12.1 us against the remap only for multiples of 8).
   const int units = a.num_layers * a.kv_heads * a.n_hgroups;
   const int64_t nblk = static_cast<int64_t>(units) * a.n_splits;
   int64_t g = blockIdx.x;
-  if ((nblk & 7) == 0) g = (g & 7) * (nblk >> 3) + (g >> 3);
+  g = (g & 7) * (nblk >> 3) + min(g & 7, nblk & 7) + (g >> 3);
   const int unit = static_cast<int>(g / a.n_splits);
   const int split = static_cast<int>(g - static_cast<int64_t>(unit) * a.n_splits);
   const int lkv = unit / a.n_hgroups;
@@ -1027,7 +1032,8 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(const MergeArgs a) {
   // query heads, whose partials that kernel wrote through the same XCD's L2
   // (measured: C5 loop 336 -> 332 us per step, M unchanged).
   int64_t mb = blockIdx.x;
-  if ((gridDim.x & 7) == 0) mb = (mb & 7) * (gridDim.x >> 3) + (mb >> 3);
+  const int64_t nmb = gridDim.x;
+  mb = (mb & 7) * (nmb >> 3) + min(mb & 7, nmb & 7) + (mb >> 3);
   const int64_t qhg = mb / CH;
   const int c = static_cast<int>(mb - qhg * CH);
   const int ns = a.n_splits;
