@@ -289,11 +289,18 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   const int t1 = static_cast<int>(a.seq_len);
   const int BSTRIDE = a.n_splits * kStride;
   const int n_blocks = (t1 + kStride - 1) / kStride;
-  const int n_iter = split < n_blocks ? (n_blocks - split + a.n_splits - 1) / a.n_splits : 0;
+  // In append mode split 0 also packs the new token, so it takes the
+  // lightest share (the blocks split n_splits - 1 would take) and splits
+  // 1.. the shares of splits 0..: the extra block of a length that does not
+  // divide evenly lands on a split without the append work (4-layer decode
+  // loop at 32768 + t tokens x 8 KV heads, 32 splits: 65.0-65.8 -> 62.2-62.4
+  // us per step).
+  const int deal = a.new_k != nullptr ? (split == 0 ? a.n_splits - 1 : split - 1) : split;
+  const int n_iter = deal < n_blocks ? (n_blocks - deal + a.n_splits - 1) / a.n_splits : 0;
   const int n_tiles = n_iter * kTilesPerBlock;
   auto tile_row = [&](int k) {
     const unsigned uk = static_cast<unsigned>(k);
-    return split * kStride + static_cast<int>(uk / kTilesPerBlock) * BSTRIDE + static_cast<int>(uk % kTilesPerBlock) * kTile;
+    return deal * kStride + static_cast<int>(uk / kTilesPerBlock) * BSTRIDE + static_cast<int>(uk % kTilesPerBlock) * kTile;
   };
   const uint8_t* kbase = a.k + static_cast<int64_t>(lkv) * a.cap * ROW;
   const uint8_t* vbase = a.v + static_cast<int64_t>(lkv) * a.cap * ROW;
