@@ -435,7 +435,7 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16-hilo-split/f32-acc" if loop_kernel.startswith("decode_mx_kernel") else "f32",
         "arithmetic": (
             "float32 accumulation of exact float16 hi/lo split products (16x16x32 matrix cores); "
             "softmax, merge and rotations in float32" if matrix_kernel else
@@ -579,6 +579,9 @@ def main() -> int:
     out = torch.empty((L, hq, d), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     fn = _lib.load().tq_decode_scaled_timed if scaled else _lib.load().tq_decode_timed
+    # unscaled calls bind the caller's events to the merge launch as well (tq_decode_step_timed), so a step's
+    # time is the split kernel's plus the merge kernel's
+    step_fn = None if scaled else _lib.load().tq_decode_step_timed
     flags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT
     call_args = []
     for i in range(n_rep):
@@ -596,6 +599,8 @@ def main() -> int:
             a = call_args[i % n_rep]
             if events is None:
                 rc = fn(*a, None, None)
+            elif step_fn is not None:
+                rc = step_fn(*a, *events[i])
             else:
                 rc = fn(*a, events[i][0], events[i][1])
             if rc != 0:
@@ -617,13 +622,18 @@ def main() -> int:
 
     # kernel durations: events bound to each launch (hipExtLaunchKernel start/stop)
     n_ev = min(args.steps, 200)
-    evs = [(hip.event(), hip.event()) for _ in range(n_ev)]
+    evs = [(hip.event(), hip.event(), hip.event(), hip.event()) for _ in range(n_ev)]
     torch.cuda.synchronize()
     run(n_ev, evs)
     torch.cuda.synchronize()
-    kern_ms = np.array([hip.elapsed_ms(a, b) for a, b in evs])
+    kern_ms = np.array([hip.elapsed_ms(e[0], e[1]) for e in evs])
     kern_us = float(np.mean(kern_ms) * 1e3)
     kern_med_us = float(np.median(kern_ms) * 1e3)
+    merge_us = None
+    if step_fn is not None and n_splits > 1:
+        merge_us = float(np.mean([hip.elapsed_ms(e[2], e[3]) for e in evs]) * 1e3)
+    elif n_splits == 1:
+        merge_us = 0.0
     achieved = algo_bytes / (kern_us * 1e-6) / 1e9
     kernel_name = _lib.split_kernel(hkv, hq, d, bits, flags | (_lib.TQ_F32_PRODUCTS if scaled else 0), _lib.TQ_F16, s,
                                     num_layers=L, n_splits=n_splits)
@@ -633,6 +643,8 @@ def main() -> int:
     traffic, traffic_src = measured_traffic(kernel_name, args.workload)
     log(f"decode kernel {kernel_name}: mean {kern_us:.2f} us (median {kern_med_us:.2f}), "
         f"wall {ms_per_step * 1e3:.2f} us/step (host enqueue {t_enq * 1e6 / args.steps:.2f} us/step)")
+    if merge_us is not None:
+        log(f"merge kernel mean {merge_us:.2f} us; step (split + merge) {kern_us + merge_us:.2f} us")
 
     f32_products = None
     if matrix_kernel:
@@ -672,7 +684,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16-hilo-split/f32-acc" if matrix_kernel else "f32",
         "arithmetic": (
             "float32 accumulation of exact float16 hi/lo split products (16x16x32 matrix cores); "
             "softmax, merge and rotations in float32" if matrix_kernel else
@@ -706,6 +718,12 @@ def main() -> int:
             "traffic_source": traffic_src,
             "kernel": kernel_name,
             "algorithmic_bytes_per_launch": algo_bytes,
+            # frac above: the split kernel alone (the dominant kernel); below: one whole decode step as the
+            # reference's metric times it, the split kernel plus the merge kernel (event-timed means)
+            "merge_us": None if merge_us is None else round(merge_us, 3),
+            "step_us": None if merge_us is None else round(kern_us + merge_us, 3),
+            "step_frac": None if merge_us is None else round(
+                algo_bytes / ((kern_us + merge_us) * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
         },
         "roofline_compute": compute_roofline(matrix_kernel, L, hkv, hq, d, s, kern_us),
     }

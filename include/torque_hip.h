@@ -2,10 +2,13 @@
  * torque_hip.h -- C ABI of the MI355X (gfx950) packed rotated KV-cache decode path.
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t.
- * The library allocates nothing; the caller owns all buffers (slabs,
- * centroids, signs, workspaces, outputs).  Its only device state is the fixed
- * per-GPU scratch array of tq_decode_noalloc, the entry point for callers that
- * cannot allocate a workspace.  Kernels are
+ * The library allocates no device memory; the caller owns all buffers
+ * (slabs, centroids, signs, workspaces, outputs).  Its only device state is
+ * the fixed per-GPU scratch array of tq_decode_noalloc, the entry point for
+ * callers that cannot allocate a workspace.  Its only other state is one pair
+ * of HIP events per device, created on the first timed call there that passes
+ * no merge events of its own (tq_decode_timed, tq_decode_scaled_timed,
+ * tq_decode_dense_timed) and shared by every stream.  Kernels are
  * launched asynchronously on `stream`.  Return value: TQ_OK (0) or a negative
  * TQ_ERR_* code; tq_last_error() gives the message (thread-local).
  *
@@ -30,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TQ_ABI_VERSION 3
+#define TQ_ABI_VERSION 4
 
 enum {
   TQ_OK = 0,
@@ -51,8 +54,22 @@ enum { TQ_ROTATE_KEYS = 1, TQ_ROTATE_VALUES = 2 };
  * head_dim 256); elsewhere the float32 split kernel runs.  Both accumulate in float32.  TQ_F32_PRODUCTS selects
  * the float32 kernel, TQ_MATRIX_PRODUCTS the matrix kernel wherever it can
  * run (the two exclude each other: TQ_ERR_BAD_ARG).  tq_decode_scaled always
- * runs the float32 split kernel. */
-enum { TQ_ROTATE_QUERY = 1, TQ_INVERSE_OUTPUT = 2, TQ_F32_PRODUCTS = 4, TQ_MATRIX_PRODUCTS = 8 };
+ * runs the float32 split kernel.
+ *
+ * Reproducibility: the float32 split kernel and the merge always sum in a
+ * fixed order, so their outputs are bit-identical from call to call (as the
+ * reference's decode is, cache.py:98-140, mlx_ops.py:571-595).  The matrix
+ * kernel's wavefronts claim tiles dynamically by default, so the order of its
+ * sums, and the last bits of the output, can change between calls (outputs
+ * agree to float32 rounding).  TQ_DETERMINISTIC deals its tiles statically:
+ * bit-identical outputs on every call and every graph replay. */
+enum {
+  TQ_ROTATE_QUERY = 1,
+  TQ_INVERSE_OUTPUT = 2,
+  TQ_F32_PRODUCTS = 4,
+  TQ_MATRIX_PRODUCTS = 8,
+  TQ_DETERMINISTIC = 16
+};
 
 int tq_abi_version(void);
 const char* tq_last_error(void);
@@ -182,7 +199,9 @@ int tq_decode(const void* query, int query_dtype, int num_layers, int query_head
  * more than 8 MiB (tq_decode_workspace_bytes) returns TQ_ERR_BAD_ARG before
  * any launch; pass fewer splits or fewer layers.  Every call on one GPU shares
  * that GPU's scratch: calls that overlap on one GPU (different streams, or
- * threads without ordering) race and must not be issued. */
+ * threads without ordering) race and must not be issued.  The first call on a
+ * device must be made outside stream capture (it looks the scratch address
+ * up); made inside one, it returns TQ_ERR_BAD_ARG before enqueueing anything. */
 int tq_decode_noalloc(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
                       int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
                       int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,
@@ -236,15 +255,32 @@ int tq_decode_append(const void* query, int query_dtype, const void* new_keys, c
  * kernel itself, so hipEventElapsedTime gives its execution time (the merge
  * kernel, when launched, follows it on the stream).  When either event is
  * given, the merge launch is profiled as well, with a pair of events the
- * library owns (one pair per device): a dispatch with profiling that follows
- * one without starts late on most of the GPU's XCDs, and the split kernel's
- * events would count that delay as its own time. */
+ * library owns (one pair per device, shared by every stream of that device and
+ * never read): a dispatch with profiling that follows one without starts late
+ * on most of the GPU's XCDs, and the split kernel's events would count that
+ * delay as its own time.  tq_decode_step_timed takes the merge's events from
+ * the caller instead. */
 int tq_decode_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
                     int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
                     int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,
                     const float* signs_left, const float* signs_right, int flags, const float* current_keys,
                     const float* current_values, int n_splits, void* workspace, size_t workspace_bytes, float* out,
                     hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+
+/* tq_decode with caller-owned HIP events bound to each of its launches:
+ * split_start / split_stop to the split kernel, merge_start / merge_stop to
+ * the merge kernel (both NULL: the library's pair, as in tq_decode_timed;
+ * one NULL: TQ_ERR_BAD_ARG).  A call that resolves to one split launches no
+ * merge kernel and records neither merge event.  The time of one decode step
+ * is the sum of the two kernels' elapsed times.  For benchmarks; no reference
+ * counterpart. */
+int tq_decode_step_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
+                         int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
+                         int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,
+                         const float* signs_left, const float* signs_right, int flags, const float* current_keys,
+                         const float* current_values, int n_splits, void* workspace, size_t workspace_bytes,
+                         float* out, hipStream_t stream, hipEvent_t split_start, hipEvent_t split_stop,
+                         hipEvent_t merge_start, hipEvent_t merge_stop);
 
 /* Dense-KV decode attention with the same split-K structure, for float16 or
  * float32 K/V slabs [L, Hkv, capacity, D].  With kv_dtype TQ_F16 this is the

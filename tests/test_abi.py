@@ -45,7 +45,7 @@ def test_host_only_entry_points():
     from torque_hip import _lib
 
     lib = _lib.load()
-    assert lib.tq_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.tq_abi_version() == _lib.ABI_VERSION == 4
     # 4-bit rows in groups of 4 query heads: the f16-split matrix kernel, one 768-thread workgroup per CU
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, 0, 32768, 256) == 32
     # the float32-product kernel (requested, or 3-bit rows): two 256-thread workgroups per CU
@@ -99,6 +99,15 @@ def test_host_only_entry_points():
     assert ks(8, 32, 128, 3, mx, _lib.TQ_F16, 32768) == "decode_kernel<PackedB3,128,4>"
     with pytest.raises(ValueError):
         _lib.split_kernel(8, 30, 128, 4, 0, _lib.TQ_F16, 100)
+    # the two product flags exclude each other in the host queries as in tq_decode
+    with pytest.raises(ValueError, match="exclude each other"):
+        _lib.split_kernel(8, 32, 128, 4, mx | f32, _lib.TQ_F16, 32768)
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, mx | f32, 32768, 256) == _lib.TQ_ERR_BAD_ARG
+    assert b"exclude each other" in lib.tq_last_error()
+    # TQ_DETERMINISTIC changes neither the kernel nor the plan
+    det = _lib.TQ_DETERMINISTIC
+    assert ks(8, 32, 128, 4, det, _lib.TQ_F16, 32768) == "decode_mx_kernel<128,true>"
+    assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, det, 32768, 256) == 32
 
 
 @pytest.mark.parametrize(

@@ -113,9 +113,12 @@ def test_mixed_kv_dtypes_quantize_at_float32(hip_device):
 @pytest.mark.parametrize("bits,head_dim", [(4, 128), (4, 256), (2, 128)])
 def test_decode_append_against_oracle_and_split_counts(hip_device, bits, head_dim):
     """3000 rows: 1 and 3 splits run the matrix kernel (24 and 8 blocks of 128 rows per split), 64 splits the
-    float32 kernel; every output matches the oracle's append-then-decode."""
+    float32 kernel; 5 and 7 splits force the matrix kernel onto uneven shares (24 blocks: 5/5/5/5/4 and
+    4/4/4/3/3/3/3), where the appending split 0 takes the lightest one.  Every output matches the oracle's
+    append-then-decode."""
     import torque_hip as th
     from torque_hip import _lib
+    from torque_hip.ops import packed_decode_append
 
     D = head_dim
 
@@ -132,16 +135,29 @@ def test_decode_append_against_oracle_and_split_counts(hip_device, bits, head_di
     kernels = [_lib.split_kernel(2, 8, D, bits, 3, _lib.TQ_F32, 3000, n_splits=ns) for ns in (1, 3, 64)]
     mx_name = f"decode_mx_kernel<{D},false>" if bits == 4 else f"decode_mx_kernel<{D},false,{bits}>"
     assert kernels[:2] == [mx_name] * 2 and kernels[2].startswith("decode_kernel<"), kernels
+    forced = (5, 7)
+    for ns in forced:
+        assert _lib.split_kernel(2, 8, D, bits, 3 | _lib.TQ_MATRIX_PRODUCTS, _lib.TQ_F32, 3000, n_splits=ns) == mx_name
+    qd = torch.from_numpy(q).to(hip_device).reshape(1, 8, D)
+    knd = torch.from_numpy(kn).to(hip_device).reshape(1, 2, 1, D)
+    vnd = torch.from_numpy(vn).to(hip_device).reshape(1, 2, 1, D)
+    split_counts = (1, 3, 64) + forced
     outs = []
-    for ns in (1, 3, 64):
+    for ns in split_counts:
         st.length = 3000  # rewrite the same token at the same row each time
-        outs.append(
-            st.decode_append(torch.from_numpy(q).to(hip_device).reshape(1, 8, D),
-                             torch.from_numpy(kn).to(hip_device).reshape(1, 2, 1, D),
-                             torch.from_numpy(vn).to(hip_device).reshape(1, 2, 1, D),
-                             rotate_query=True, inverse_output=True, rotate_keys=True, rotate_values=True,
-                             n_splits=ns).cpu().numpy()[0]
-        )
+        if ns in forced:
+            got = packed_decode_append(
+                qd, knd, vnd, num_layers=1, query_heads=8, kv_heads=2, head_dim=D, bit_width=bits,
+                key_codes=st.key_codes, value_codes=st.value_codes, capacity=st.capacity, seq_len=3000,
+                key_centroids=st.key_centroids, value_centroids=st.value_centroids,
+                key_boundaries=st.key_boundaries, value_boundaries=st.value_boundaries,
+                signs_left=st.signs_left, signs_right=st.signs_right, rotate_query=True, inverse_output=True,
+                n_splits=ns, matrix_products=True)
+            st.length = 3001
+        else:
+            got = st.decode_append(qd, knd, vnd, rotate_query=True, inverse_output=True, rotate_keys=True,
+                                   rotate_values=True, n_splits=ns)
+        outs.append(got.cpu().numpy()[0])
     model = o.OracleCache(bit_width=bits, head_dim=D, num_layers=1, kv_heads=2,
                           key_centroids=cache.key_codebook.centroids, value_centroids=cache.value_codebook.centroids,
                           signs_left=cache.rotation.signs_left, signs_right=cache.rotation.signs_right)
@@ -151,7 +167,7 @@ def test_decode_append_against_oracle_and_split_counts(hip_device, bits, head_di
     kc, vc = _codes(cache)
     np.testing.assert_array_equal(kc.view(np.uint32), model.k_codes)
     np.testing.assert_array_equal(vc.view(np.uint32), model.v_codes)
-    for ns, out in zip((1, 3, 64), outs):
+    for ns, out in zip(split_counts, outs):
         np.testing.assert_allclose(out, exp, atol=2e-6, rtol=1e-5, err_msg=f"n_splits {ns}")
 
 

@@ -6,8 +6,9 @@ kernel + merge kernel) and the allocation-free ``tq_decode_noalloc`` -- the
 entry point meant for callers that capture -- are each captured once and
 replayed several times, with the program's own eager decodes and
 synchronisations between the replays.  Every replay must give the eager
-result: bit for bit on the float32-product kernel (its work split is static),
-to float32 rounding on the matrix kernel (its wavefronts claim tiles
+result: bit for bit on the float32-product kernel (its work split is static)
+and on the matrix kernel with TQ_DETERMINISTIC (static tile deal), to
+float32 rounding on the matrix kernel's default (its wavefronts claim tiles
 dynamically).  The eager calls in between run other inputs and shapes, so a
 replay that read state an earlier call left behind (workspace, scratch)
 would show.
@@ -34,7 +35,7 @@ def _cache(dev, bits, head_dim, kv_heads, seq_len, seed):
     return cache
 
 
-def _decode(cache, query, f32_products):
+def _decode(cache, query, f32_products, deterministic=False):
     from torque_hip.ops import packed_decode
 
     st, cfg = cache._store, cache.config
@@ -43,7 +44,8 @@ def _decode(cache, query, f32_products):
                          value_codes=st.value_codes, capacity=st.capacity, seq_len=st.length,
                          key_centroids=st.key_centroids, value_centroids=st.value_centroids,
                          signs_left=st.signs_left, signs_right=st.signs_right, rotate_query=True,
-                         inverse_output=True, f32_products=f32_products, matrix_products=not f32_products)
+                         inverse_output=True, f32_products=f32_products, matrix_products=not f32_products,
+                         deterministic=deterministic)
 
 
 def _noalloc(cache, query, out):
@@ -82,19 +84,19 @@ def _check(got, ref, exact, what):
         np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max(), err_msg=what)
 
 
-@pytest.mark.parametrize("f32_products", [True, False])
-def test_captured_decode_replays(hip_device, f32_products):
+@pytest.mark.parametrize("f32_products,deterministic", [(True, False), (False, False), (False, True)])
+def test_captured_decode_replays(hip_device, f32_products, deterministic):
     main = _cache(hip_device, 4, 128, 8, 16384, seed=21)
     other = _cache(hip_device, 4, 256, 2, 9000, seed=22)
     gen = torch.Generator(device=hip_device).manual_seed(23)
     q = torch.randn((1, 32, 128), generator=gen, device=hip_device).half()
     q_other = torch.randn((1, 8, 256), generator=gen, device=hip_device)
-    ref = _decode(main, q, f32_products).cpu().numpy()
-    graph, out = _capture(hip_device, lambda: _decode(main, q, f32_products))
+    ref = _decode(main, q, f32_products, deterministic).cpu().numpy()
+    graph, out = _capture(hip_device, lambda: _decode(main, q, f32_products, deterministic))
     for rep in range(4):
         graph.replay()
         torch.cuda.synchronize(hip_device)
-        _check(out.cpu().numpy(), ref, f32_products, f"replay {rep}")
+        _check(out.cpu().numpy(), ref, f32_products or deterministic, f"replay {rep}")
         _decode(other, q_other, f32_products)  # eager work on other buffers between the replays
         torch.cuda.synchronize(hip_device)
 

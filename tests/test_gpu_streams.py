@@ -31,12 +31,13 @@ def _inputs(dev, seed, kv_heads, seq_len, head_dim=128, bits=4, group=4):
                 capacity=seq_len, seq_len=seq_len)
 
 
-@pytest.mark.parametrize("f32_products", [True, False])
-def test_two_streams_match_sequential(hip_device, f32_products):
+@pytest.mark.parametrize("f32_products,deterministic", [(True, False), (False, False), (False, True)])
+def test_two_streams_match_sequential(hip_device, f32_products, deterministic):
     from torque_hip.ops import packed_decode
 
     cases = [_inputs(hip_device, 1, kv_heads=8, seq_len=16384), _inputs(hip_device, 2, kv_heads=4, seq_len=20000)]
-    decode = lambda c: packed_decode(**c, f32_products=f32_products, matrix_products=not f32_products)
+    decode = lambda c: packed_decode(**c, f32_products=f32_products, matrix_products=not f32_products,
+                                     deterministic=deterministic)
     ref = [decode(c).cpu().numpy() for c in cases]
     torch.cuda.synchronize()
     s1, s2 = torch.cuda.Stream(hip_device), torch.cuda.Stream(hip_device)
@@ -47,7 +48,49 @@ def test_two_streams_match_sequential(hip_device, f32_products):
             b = decode(cases[1])
         torch.cuda.synchronize()
         for got, exp in zip((a.cpu().numpy(), b.cpu().numpy()), ref):
-            if f32_products:
+            if f32_products or deterministic:
                 np.testing.assert_array_equal(got, exp, err_msg=f"rep {rep}")
             else:
                 np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-6 * np.abs(exp).max(), err_msg=f"rep {rep}")
+
+
+def test_step_timed_binds_caller_events(hip_device):
+    """tq_decode_step_timed: the same output as tq_decode, with the caller's events bound to the split and
+    the merge launches (both elapsed times positive); one merge event alone is refused."""
+    import ctypes
+
+    from torque_hip import _lib, ops
+    from torque_hip._tensors import dtype_code
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    evs = [ctypes.c_void_p() for _ in range(4)]
+    for e in evs:
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+    c = _inputs(hip_device, 3, kv_heads=8, seq_len=16384)
+    flags = _lib.TQ_DETERMINISTIC
+    ns = ops.plan_splits(1, 8, 32, 128, 16384, hip_device, bit_width=4, flags=flags)
+    assert ns > 1
+    ws = ops.workspace_for(1, 8, 32, 128, ns, hip_device)
+    ref = ops.packed_decode(**c, n_splits=ns, deterministic=True)
+    out = torch.full_like(ref, float("nan"))
+    stream = torch.cuda.current_stream(hip_device).cuda_stream
+    args = (c["query"].data_ptr(), dtype_code(c["query"]), 1, 32, 8, 128, 4, c["key_codes"].data_ptr(),
+            c["value_codes"].data_ptr(), 16384, 16384, c["key_centroids"].data_ptr(), c["value_centroids"].data_ptr(),
+            None, None, flags, None, None, ns, ws.data_ptr(), ws.numel(), out.data_ptr(), stream)
+    _lib.call("tq_decode_step_timed", *args, *evs)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), ref.cpu().numpy())
+    for a, b in ((evs[0], evs[1]), (evs[2], evs[3])):
+        hip.hipEventSynchronize(b)
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        assert 0.0 < ms.value < 50.0
+    with pytest.raises(ValueError, match="both be given"):
+        _lib.call("tq_decode_step_timed", *args, evs[0], evs[1], evs[2], None)
+    torch.cuda.synchronize()
+    for e in evs:
+        hip.hipEventDestroy(e)

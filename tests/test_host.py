@@ -138,3 +138,53 @@ def test_artifact_manifest_errors():
         TorqueArtifactManifest.from_dict(bad)
     with pytest.raises(ValueError, match="Unsupported artifact version"):
         TorqueArtifactManifest.from_dict(_manifest_payload(format_version=2))
+
+
+# The reference package's public names (src/torque_mlx/__init__.py:38-68), split by
+# whether they sit on the packed decode path this package replaces.
+REFERENCE_EXPORTS_IN_SCOPE = (
+    "QwenDecodeBenchmarkProfile",  # qwen_benchmark.py:40-105
+    "QwenDecodeRuntimeBenchmarkResult",  # qwen_benchmark.py:128-176
+    "QwenInspectionReport",  # families/qwen.py:31-78 (read by the qwen-decode profile loader)
+    "QwenModelArtifactManifest",  # families/qwen.py:81-229 (the manifest feeding build_cache)
+    "TorqueArtifact",
+    "TorqueArtifactManifest",
+    "TorqueConfig",
+    "TorqueKVCache",
+    "TorqueKVCacheMLX",
+    "decode_packed_attention",
+    "inspect_qwen_hf_directory",
+    "load_qwen_decode_benchmark_profile",
+    "load_qwen_model_manifest",
+    "load_torque_artifact",
+    "metal_available",
+    "run_qwen_decode_runtime_benchmark",
+    "run_synthetic_decode_benchmark",
+)
+# Conversion, weight fusion, Qwen text evaluation and artifact writing: not on the decode path,
+# deliberately absent.
+REFERENCE_EXPORTS_OUT_OF_SCOPE = (
+    "FusedAttentionWeights",
+    "QwenTextBenchmarkCase",
+    "QwenTextBenchmarkComparison",
+    "QwenTextPerplexityResult",
+    "benchmark_qwen_text_models",
+    "build_torque_artifact",
+    "convert_npz_checkpoint",
+    "convert_qwen_attention_layer",
+    "convert_qwen_model",
+    "evaluate_artifact",
+    "evaluate_qwen_text_perplexity",
+    "fuse_attention_weights",
+)
+
+
+def test_reference_exports_resolve():
+    """`import torque_hip as torque_mlx` resolves every decode-path name of the reference's __all__."""
+    assert len(REFERENCE_EXPORTS_IN_SCOPE) + len(REFERENCE_EXPORTS_OUT_OF_SCOPE) == 29
+    for name in REFERENCE_EXPORTS_IN_SCOPE:
+        assert hasattr(th, name), name
+        assert name in th.__all__, name
+    for name in REFERENCE_EXPORTS_OUT_OF_SCOPE:
+        assert not hasattr(th, name), name
+    assert callable(th.run_synthetic_decode_benchmark) and callable(th.run_qwen_decode_runtime_benchmark)

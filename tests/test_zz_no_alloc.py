@@ -76,3 +76,106 @@ def test_noalloc_rejects_oversized_plan(hip_device):
     with pytest.raises(ValueError, match="bytes of scratch"):
         _lib.call("tq_decode_noalloc", fake, 0, 4, 64, 8, 256, 4, fake, fake, 1 << 20, 1 << 20, fake, fake, None, None,
                   0, None, None, 256, fake, None)
+
+
+def test_noalloc_deterministic_matches_decode_bit_for_bit(hip_device):
+    """With TQ_DETERMINISTIC both entry points sum the same tiles in the same order: identical bits, on two
+    calls in a row (the second smaller)."""
+    from torque_hip import _lib
+    from torque_hip._tensors import dtype_code
+
+    big = _cache(hip_device, 4, 128, 4, 6000, seed=13)
+    small = _cache(hip_device, 2, 128, 2, 1500, seed=14)
+    gen = torch.Generator(device=hip_device).manual_seed(15)
+    stream = torch.cuda.current_stream(hip_device).cuda_stream
+    flags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT | _lib.TQ_DETERMINISTIC | _lib.TQ_MATRIX_PRODUCTS
+    for cache, hq, ns in ((big, 16, 6), (small, 8, 3)):
+        st, cfg = cache._store, cache.config
+        q = torch.randn((1, hq, cfg.head_dim), generator=gen, device=hip_device).half()
+        common = (q.data_ptr(), dtype_code(q), 1, hq, cfg.kv_heads, cfg.head_dim, cfg.bit_width,
+                  st.key_codes.data_ptr(), st.value_codes.data_ptr(), st.capacity, st.length,
+                  st.key_centroids.data_ptr(), st.value_centroids.data_ptr(), st.signs_left.data_ptr(),
+                  st.signs_right.data_ptr(), flags, None, None, ns)
+        ws = torch.empty(_lib.call("tq_decode_workspace_bytes", 1, cfg.kv_heads, hq, cfg.head_dim, ns, 0),
+                         dtype=torch.uint8, device=hip_device)
+        ref = torch.empty((1, hq, cfg.head_dim), dtype=torch.float32, device=hip_device)
+        got = torch.full_like(ref, float("nan"))
+        _lib.call("tq_decode", *common, ws.data_ptr(), ws.numel(), ref.data_ptr(), stream)
+        _lib.call("tq_decode_noalloc", *common, got.data_ptr(), stream)
+        torch.cuda.synchronize(hip_device)
+        np.testing.assert_array_equal(got.cpu().numpy(), ref.cpu().numpy())
+
+
+_FIRST_CALL_IN_CAPTURE = r"""
+import sys
+import numpy as np
+import torch
+import torque_hip as th
+from torque_hip import _lib
+from torque_hip._tensors import dtype_code
+
+dev = torch.device("cuda", 0)
+cfg = th.TorqueConfig(bit_width=4, head_dim=128, num_layers=1, kv_heads=2)
+cache = th.TorqueKVCacheHIP(config=cfg, initial_capacity=2048, decode_tail_capacity=0)
+gen = torch.Generator(device=dev).manual_seed(1)
+cache.append_many(key=torch.randn((1, 2, 2048, 128), generator=gen, device=dev),
+                  value=torch.randn((1, 2, 2048, 128), generator=gen, device=dev))
+st = cache._store
+q = torch.randn((1, 8, 128), generator=gen, device=dev)
+out = torch.full((1, 8, 128), float("nan"), device=dev)
+flags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT | _lib.TQ_DETERMINISTIC
+
+
+def call():
+    _lib.call("tq_decode_noalloc", q.data_ptr(), dtype_code(q), 1, 8, 2, 128, 4, st.key_codes.data_ptr(),
+              st.value_codes.data_ptr(), st.capacity, st.length, st.key_centroids.data_ptr(),
+              st.value_centroids.data_ptr(), st.signs_left.data_ptr(), st.signs_right.data_ptr(), flags, None, None,
+              0, out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+
+
+torch.cuda.synchronize()
+print("first call inside a capture", flush=True)
+graph = torch.cuda.CUDAGraph()
+try:
+    with torch.cuda.graph(graph):
+        call()
+except ValueError as e:
+    assert "inside a stream capture" in str(e), e
+    print("refused:", e, flush=True)
+else:
+    sys.exit("the first call inside a capture was not refused")
+torch.cuda.synchronize()
+call()  # eager: looks the scratch address up
+torch.cuda.synchronize()
+ref = out.clone()
+assert torch.isfinite(ref).all()
+out.fill_(float("nan"))
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    call()
+for _ in range(3):
+    out.fill_(float("nan"))
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+print("ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_capture_is_refused(hip_device):
+    """In a fresh process the first tq_decode_noalloc call on a device looks its scratch address up; made
+    inside a stream capture it is refused with a message before anything is enqueued, and after one eager
+    call the same call captures and replays."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    repo = Path(__file__).resolve().parents[1]
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([str(repo / "torque-mlx_amd"), str(repo), env.get("PYTHONPATH", "")])
+    print("child: first tq_decode_noalloc call inside torch.cuda.graph", flush=True)
+    proc = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE], env=env, capture_output=True, text=True,
+                          timeout=110)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "refused:" in proc.stdout and proc.stdout.rstrip().endswith("ok"), proc.stdout

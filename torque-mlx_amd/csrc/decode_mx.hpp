@@ -388,10 +388,18 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   int* s_claim = reinterpret_cast<int*>(s_misc + 8);
   if (tid == 0) *s_claim = kPrefetch * NW;  // first dynamic claim; read only after the set-up barrier
   // lane 0 takes the next tile; the value is read (readfirstlane) only where
-  // the tile is loaded, one iteration later, so the atomic's latency hides
+  // the tile is loaded, one iteration later, so the atomic's latency hides.
+  // With a static deal (TQ_DETERMINISTIC) wavefront w takes tiles w, w + NW,
+  // w + 2 NW, ...: every call sums the same tiles in the same order.
+  int next_static = kPrefetch * NW + wave;
   auto claim = [&]() {
     int k = 0;
-    if (lane == 0) k = atomicAdd(s_claim, 1);
+    if (a.static_deal) {
+      k = next_static;
+      next_static += NW;
+    } else if (lane == 0) {
+      k = atomicAdd(s_claim, 1);
+    }
     return k;
   };
 

@@ -231,6 +231,9 @@ struct DecodeArgs {
   const float* k_scales;
   const float* v_scales;
   int wide_iter;  // host side only: launch the kWideTokensPerIter instance
+  // decode_mx_kernel: deal every tile statically (TQ_DETERMINISTIC), so the
+  // summation order, and with it every output bit, is the same on every call
+  int static_deal;
 };
 
 // Finish one output row held by a wavefront: optional extra dense token
@@ -1298,31 +1301,37 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// The current device's scratch address (looked up on the first call on that
-// device), or nullptr with the error set.
-void* device_scratch() {
+// The current device's scratch address in *out (looked up on the first call
+// on that device), or an error code with the message set.  The lookup is not a stream
+// operation, but it may load the code object, which a stream capture does not
+// allow: a first call on a device made inside a capture is refused with a
+// message, before anything is enqueued.
+int device_scratch(hipStream_t stream, void** out) {
   int dev = -1;
   const hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
-    fail(TQ_ERR_LAUNCH, std::string("tq_decode_noalloc: no current HIP device: ") + hipGetErrorString(e));
-    return nullptr;
+    return fail(TQ_ERR_LAUNCH, std::string("tq_decode_noalloc: no current HIP device: ") + hipGetErrorString(e));
   }
   if (dev < 0 || dev >= kMaxDevices) {
-    fail(TQ_ERR_UNSUPPORTED, "tq_decode_noalloc: device index " + std::to_string(dev) + " out of range");
-    return nullptr;
+    return fail(TQ_ERR_UNSUPPORTED, "tq_decode_noalloc: device index " + std::to_string(dev) + " out of range");
   }
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
+      return fail(TQ_ERR_BAD_ARG, "tq_decode_noalloc: the first call on device " + std::to_string(dev) +
+                                      " is inside a stream capture; make one call on that device outside capture first");
+    }
     void* ptr = nullptr;
     const hipError_t r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (r != hipSuccess || ptr == nullptr) {
-      fail(TQ_ERR_LAUNCH, std::string("tq_decode_noalloc: hipGetSymbolAddress(scratch) failed: ") +
-                              hipGetErrorString(r));
-      return nullptr;
+      return fail(TQ_ERR_LAUNCH, std::string("tq_decode_noalloc: hipGetSymbolAddress(scratch) failed: ") +
+                                     hipGetErrorString(r));
     }
     g_scratch_ptr[dev] = ptr;
   }
-  return g_scratch_ptr[dev];
+  *out = g_scratch_ptr[dev];
+  return TQ_OK;
 }
 
 // Rows per workgroup iteration of decode_kernel for `fmt` (2/3/4 packed
@@ -1511,8 +1520,11 @@ struct AppendSpec {
 
 int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hipStream_t stream, hipEvent_t start,
                 hipEvent_t stop);
+struct ProfileEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
 int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream,
-                 bool profiled);
+                 bool profiled, const ProfileEvents* caller_events);
 
 template <int D, bool QF16, int BITS>
 void launch_mx_t(const DecodeArgs& a, dim3 grid, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
@@ -1564,7 +1576,8 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
                   int flags, const float* cur_k, const float* cur_v, int n_splits, void* workspace,
                   size_t workspace_bytes, float* out, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
                   const AppendSpec* app = nullptr,
-                  const float* k_scales = nullptr, const float* v_scales = nullptr) {
+                  const float* k_scales = nullptr, const float* v_scales = nullptr,
+                  const ProfileEvents* merge_events = nullptr) {
   int rc = check_geometry(head_dim, 0);
   if (rc) return rc;
   if ((k_scales == nullptr) != (v_scales == nullptr))
@@ -1649,6 +1662,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   }
   a.n_splits = p.n_splits;
   a.wide_iter = p.tokens_per_iter == kWideTokensPerIter;
+  a.static_deal = (flags & TQ_DETERMINISTIC) != 0;
   a.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
   a.ws_acc = reinterpret_cast<float*>(ws + wl.acc);
   a.ws_cur_s = reinterpret_cast<float*>(ws + wl.cur_s);
@@ -1674,7 +1688,7 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   if (rc) return rc;
   rc = launch_status("decode_kernel");
   if (rc || p.n_splits == 1) return rc;
-  return launch_merge(m, num_layers, query_heads, head_dim, stream, start != nullptr || stop != nullptr);
+  return launch_merge(m, num_layers, query_heads, head_dim, stream, start != nullptr || stop != nullptr, merge_events);
 }
 
 int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hipStream_t stream, hipEvent_t start,
@@ -1702,17 +1716,15 @@ int launch_fp32(const DecodeArgs& a, int fmt, int head_dim, int hg, int nblk, hi
   return rc;
 }
 
-// Events of the merge launch of a timed call, one pair per device (created on
-// first use with that device current; never read).  A timed call launches
+// Events of the merge launch of a timed call whose caller passes none, one
+// pair per device (created on first use with that device current; never
+// read, and shared by every stream of the device).  A timed call launches
 // the merge kernel with profiling too: a dispatch launched with profiling
 // events right after one launched without starts on six of the eight XCDs
 // about 1.2 us after the other two (measured on MI355X for the split kernel
 // after an unprofiled merge: median workgroup start skew 1.25 us, against
 // 0.13 us with no events and 0.15 us with every dispatch profiled), and the
 // split kernel's events would count that delay as its own time.
-struct ProfileEvents {
-  hipEvent_t start = nullptr, stop = nullptr;
-};
 std::mutex g_profile_mutex;
 ProfileEvents g_merge_events[kMaxDevices];
 
@@ -1748,15 +1760,17 @@ void launch_merge_d(const MergeArgs& m, unsigned mblk, hipStream_t stream, const
 }
 
 int launch_merge(const MergeArgs& m, int num_layers, int query_heads, int head_dim, hipStream_t stream,
-                 bool profiled) {
+                 bool profiled, const ProfileEvents* caller_events) {
   const unsigned mblk =
       static_cast<unsigned>(static_cast<int64_t>(num_layers) * query_heads * (head_dim / kMergeDims));
   ProfileEvents ev;
-  if (profiled) {
+  if (caller_events != nullptr) {
+    ev = *caller_events;
+  } else if (profiled) {
     const int rc = merge_profile_events(&ev);
     if (rc) return rc;
   }
-  const ProfileEvents* evp = profiled ? &ev : nullptr;
+  const ProfileEvents* evp = (profiled || caller_events != nullptr) ? &ev : nullptr;
   switch (head_dim) {
     case 64:
       launch_merge_d<64>(m, mblk, stream, evp);
@@ -2188,6 +2202,8 @@ int tq_decode_default_splits(int num_layers, int kv_heads, int query_heads, int 
                              int64_t seq_len, int num_cus) {
   if (num_layers <= 0 || kv_heads <= 0 || query_heads <= 0 || query_heads % kv_heads != 0)
     return fail(TQ_ERR_BAD_ARG, "bad head configuration");
+  if ((flags & TQ_F32_PRODUCTS) != 0 && (flags & TQ_MATRIX_PRODUCTS) != 0)
+    return fail(TQ_ERR_BAD_ARG, "TQ_F32_PRODUCTS and TQ_MATRIX_PRODUCTS exclude each other");
   const int group = query_heads / kv_heads;
   const int hg = pick_hg(group);
   const int units = num_layers * kv_heads * (group / hg);
@@ -2205,6 +2221,10 @@ const char* tq_decode_split_kernel(int num_layers, int kv_heads, int query_heads
   const bool packed = bits == 2 || bits == 3 || bits == 4;
   if (!packed) {
     fail(TQ_ERR_UNSUPPORTED, "split kernel names cover packed rows (bits 2, 3, 4)");
+    return nullptr;
+  }
+  if ((flags & TQ_F32_PRODUCTS) != 0 && (flags & TQ_MATRIX_PRODUCTS) != 0) {
+    fail(TQ_ERR_BAD_ARG, "TQ_F32_PRODUCTS and TQ_MATRIX_PRODUCTS exclude each other");
     return nullptr;
   }
   const int group = query_heads / kv_heads;
@@ -2272,8 +2292,9 @@ int tq_decode_noalloc(const void* query, int query_dtype, int num_layers, int qu
                                     " bytes of scratch (" + std::to_string(p.n_splits) +
                                     " splits) but the static scratch holds " + std::to_string(kScratchBytes) +
                                     "; pass fewer splits or decode fewer layers per call");
-  void* ws = device_scratch();
-  if (ws == nullptr) return TQ_ERR_LAUNCH;
+  void* ws = nullptr;
+  rc = device_scratch(stream, &ws);
+  if (rc) return rc;
   return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes,
                        value_codes, capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, flags,
                        current_keys, current_values, p.n_splits, ws, kScratchBytes, out, stream, nullptr, nullptr);
@@ -2334,6 +2355,25 @@ int tq_decode_timed(const void* query, int query_dtype, int num_layers, int quer
   return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes,
                        value_codes, capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, flags,
                        current_keys, current_values, n_splits, workspace, workspace_bytes, out, stream, start, stop);
+}
+
+int tq_decode_step_timed(const void* query, int query_dtype, int num_layers, int query_heads, int kv_heads,
+                         int head_dim, int bits, const uint32_t* key_codes, const uint32_t* value_codes,
+                         int64_t capacity, int64_t seq_len, const float* key_centroids, const float* value_centroids,
+                         const float* signs_left, const float* signs_right, int flags, const float* current_keys,
+                         const float* current_values, int n_splits, void* workspace, size_t workspace_bytes,
+                         float* out, hipStream_t stream, hipEvent_t split_start, hipEvent_t split_stop,
+                         hipEvent_t merge_start, hipEvent_t merge_stop) {
+  if (!valid_bits(bits)) return fail(TQ_ERR_UNSUPPORTED, "Unsupported bit width: " + std::to_string(bits));
+  if ((merge_start == nullptr) != (merge_stop == nullptr))
+    return fail(TQ_ERR_BAD_ARG, "merge_start and merge_stop must both be given or both be null");
+  ProfileEvents mev;
+  mev.start = merge_start;
+  mev.stop = merge_stop;
+  return decode_common(bits, query, query_dtype, num_layers, query_heads, kv_heads, head_dim, key_codes,
+                       value_codes, capacity, seq_len, key_centroids, value_centroids, signs_left, signs_right, flags,
+                       current_keys, current_values, n_splits, workspace, workspace_bytes, out, stream, split_start,
+                       split_stop, nullptr, nullptr, nullptr, merge_start != nullptr ? &mev : nullptr);
 }
 
 int tq_decode_dense(const void* query, int query_dtype, const void* keys, const void* values, int kv_dtype,

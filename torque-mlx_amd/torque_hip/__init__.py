@@ -7,6 +7,7 @@ hand-written HIP kernels for gfx950 behind the C ABI in include/torque_hip.h.
 
 from torque_hip._lib import hip_available
 from torque_hip.artifact import TorqueArtifact, TorqueArtifactManifest, load_torque_artifact
+from torque_hip.benchmarking import run_synthetic_decode_benchmark
 from torque_hip.cache import TorqueKVCache
 from torque_hip.cache_hip import SUPPORTED_DECODE_STRATEGIES, TorqueKVCacheHIP, TorqueKVCacheMLX
 from torque_hip.config import TorqueConfig
@@ -19,6 +20,16 @@ from torque_hip.ops import (
     metal_available,
     quantize_and_pack_rows,
     quantize_and_pack_rows_dual,
+)
+from torque_hip.qwen_benchmark import (
+    QwenDecodeBenchmarkProfile,
+    QwenDecodeRuntimeBenchmarkResult,
+    QwenInspectionReport,
+    QwenModelArtifactManifest,
+    inspect_qwen_hf_directory,
+    load_qwen_decode_benchmark_profile,
+    load_qwen_model_manifest,
+    run_qwen_decode_runtime_benchmark,
 )
 from torque_hip.quantization import (
     Codebook,
@@ -34,6 +45,10 @@ __all__ = [
     "CacheMetadata",
     "Codebook",
     "PackedKVLayout",
+    "QwenDecodeBenchmarkProfile",
+    "QwenDecodeRuntimeBenchmarkResult",
+    "QwenInspectionReport",
+    "QwenModelArtifactManifest",
     "RotationMode",
     "RotationSpec",
     "SUPPORTED_DECODE_STRATEGIES",
@@ -52,10 +67,15 @@ __all__ = [
     "decode_packed_attention_split_batched",
     "decode_packed_attention_split_batched_with_current",
     "hip_available",
+    "inspect_qwen_hf_directory",
     "kv_bytes_per_token",
+    "load_qwen_decode_benchmark_profile",
+    "load_qwen_model_manifest",
     "load_torque_artifact",
     "metal_available",
     "packed_words_for_head_dim",
     "quantize_and_pack_rows",
     "quantize_and_pack_rows_dual",
+    "run_qwen_decode_runtime_benchmark",
+    "run_synthetic_decode_benchmark",
 ]

@@ -19,7 +19,7 @@ import torch  # noqa: F401  -- load torch's HIP runtime first
 LIB_NAME = "libtorque_hip.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 TQ_OK = 0
 TQ_ERR_BAD_ARG = -1
@@ -35,6 +35,7 @@ TQ_ROTATE_QUERY = 1
 TQ_INVERSE_OUTPUT = 2
 TQ_F32_PRODUCTS = 4
 TQ_MATRIX_PRODUCTS = 8
+TQ_DETERMINISTIC = 16
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -77,6 +78,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tq_decode_timed": (
         _i,
         [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _sz, _p, _p, _p, _p],
+    ),
+    "tq_decode_step_timed": (
+        _i,
+        [_p, _i, _i, _i, _i, _i, _i, _p, _p, _i64, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _p, _sz, _p, _p, _p, _p, _p,
+         _p],
     ),
     "tq_decode_append": (
         _i,

@@ -116,8 +116,10 @@ def inspect_qwen_hf_directory(model_dir: str | Path) -> QwenInspectionReport:
 
 
 @dataclass(frozen=True)
-class QwenModelManifest:
-    """Decode-relevant fields of the converted-snapshot manifest (families/qwen.py:81-229)."""
+class QwenModelArtifactManifest:
+    """Decode-relevant fields of the converted-snapshot manifest (families/qwen.py:81-229): the runtime
+    config, the converted layers and the two codebooks that `build_cache()` needs.  The conversion-only
+    fields (tensor names, fusion modes, passthrough layers) are not read."""
 
     source_model_dir: str
     runtime_config: TorqueConfig
@@ -129,9 +131,14 @@ class QwenModelManifest:
     value_codebook: Codebook
 
 
-def load_qwen_model_manifest(model_dir: str | Path) -> QwenModelManifest:
+# Shorter name kept for callers of earlier versions of this package.
+QwenModelManifest = QwenModelArtifactManifest
+
+
+def load_qwen_model_manifest(model_dir: str | Path) -> QwenModelArtifactManifest:
+    """families/qwen.py:414-418 (decode-relevant fields only)."""
     payload: Mapping[str, Any] = json.loads((Path(model_dir) / QWEN_MODEL_MANIFEST_FILE).read_text(encoding="utf-8"))
-    return QwenModelManifest(
+    return QwenModelArtifactManifest(
         source_model_dir=str(payload["source_model_dir"]),
         runtime_config=config_from_dict(dict(payload["runtime_config"])),
         converted_layer_indices=[int(i) for i in payload["converted_layer_indices"]],
