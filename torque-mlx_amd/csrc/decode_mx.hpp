@@ -385,6 +385,14 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
       load_tile(kq[j], ring[j]);
     }
   };
+  // The query wavefronts issue their first tiles' rows right after their
+  // set-up loads (which return first): the memory starts streaming while
+  // the set-up runs.  The table writers issue theirs after writing, since a
+  // wavefront whose loads cannot issue (every CU's rows in flight) stalls,
+  // and the tables gate the set-up barrier.  Measured at M: split kernel
+  // median 11.9 -> 11.4 us; C3 and C4 unchanged.
+  if (wave < 4) prefetch();
+  __builtin_amdgcn_sched_barrier(0);
   int* s_claim = reinterpret_cast<int*>(s_misc + 8);
   if (tid == 0) *s_claim = kPrefetch * NW;  // first dynamic claim; read only after the set-up barrier
   // lane 0 takes the next tile; the value is read (readfirstlane) only where
@@ -449,11 +457,7 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
     }
     if (lane == 0) s_misc[wave] = ldexpf(1.f, -(sh_q + sh_k));  // raw score -> log2 units
   }
-  // The rows go out after each wavefront's set-up work: with every CU's
-  // prefetch in flight the memory pipeline is full, and a wavefront whose
-  // next load cannot issue stalls, so loads issued first would hold the
-  // set-up back.
-  prefetch();
+  if (wave >= 4) prefetch();
   // the set-up exchanges data through LDS only: the barrier leaves the
   // prefetched rows in flight
   lds_barrier();
