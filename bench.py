@@ -503,8 +503,22 @@ def run_loop(args, torch, th, _lib, ops, hip, dev) -> int:
             "sample": f"numpy oracle decode of layer 0 at the prefill length, {len(times)} repetitions, "
             f"median scaled by {L} layers (appends not included)",
         }
+    calibration_copies(args, torch, dev, result)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def calibration_copies(args, torch, dev, result) -> None:
+    """Five device copies of --calibration-copy-mib MiB: the known-size kernel that scales PMC byte counters."""
+    if args.calibration_copy_mib <= 0:
+        return
+    n = args.calibration_copy_mib * 2**20 // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    result["calibration_copy_bytes"] = n * 4
 
 
 def main() -> int:
@@ -801,16 +815,7 @@ def main() -> int:
             }
             log(f"cpu literal per-element path {lit * 1e6:.0f} us/step")
 
-    if args.calibration_copy_mib > 0:
-        n = args.calibration_copy_mib * 2**20 // 4
-        src = torch.randn(n, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        result["calibration_copy_bytes"] = n * 4
-        del src, dst
-
+    calibration_copies(args, torch, dev, result)
     print(json.dumps(result), flush=True)
     return 0
 
