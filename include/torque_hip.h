@@ -56,20 +56,11 @@ enum { TQ_ROTATE_KEYS = 1, TQ_ROTATE_VALUES = 2 };
  * run (the two exclude each other: TQ_ERR_BAD_ARG).  tq_decode_scaled always
  * runs the float32 split kernel.
  *
- * Reproducibility: the float32 split kernel and the merge always sum in a
- * fixed order, so their outputs are bit-identical from call to call (as the
- * reference's decode is, cache.py:98-140, mlx_ops.py:571-595).  The matrix
- * kernel's wavefronts claim tiles dynamically by default, so the order of its
- * sums, and the last bits of the output, can change between calls (outputs
- * agree to float32 rounding).  TQ_DETERMINISTIC deals its tiles statically:
- * bit-identical outputs on every call and every graph replay. */
-enum {
-  TQ_ROTATE_QUERY = 1,
-  TQ_INVERSE_OUTPUT = 2,
-  TQ_F32_PRODUCTS = 4,
-  TQ_MATRIX_PRODUCTS = 8,
-  TQ_DETERMINISTIC = 16
-};
+ * Reproducibility: both split kernels deal their work statically and the
+ * merge sums the splits in a fixed order, so a decode returns bit-identical
+ * outputs on every call, on any stream and in every graph replay, as the
+ * reference's decode does (cache.py:98-140, mlx_ops.py:571-595). */
+enum { TQ_ROTATE_QUERY = 1, TQ_INVERSE_OUTPUT = 2, TQ_F32_PRODUCTS = 4, TQ_MATRIX_PRODUCTS = 8 };
 
 int tq_abi_version(void);
 const char* tq_last_error(void);

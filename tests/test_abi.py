@@ -104,10 +104,6 @@ def test_host_only_entry_points():
         _lib.split_kernel(8, 32, 128, 4, mx | f32, _lib.TQ_F16, 32768)
     assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, mx | f32, 32768, 256) == _lib.TQ_ERR_BAD_ARG
     assert b"exclude each other" in lib.tq_last_error()
-    # TQ_DETERMINISTIC changes neither the kernel nor the plan
-    det = _lib.TQ_DETERMINISTIC
-    assert ks(8, 32, 128, 4, det, _lib.TQ_F16, 32768) == "decode_mx_kernel<128,true>"
-    assert lib.tq_decode_default_splits(1, 8, 32, 128, 4, det, 32768, 256) == 32
 
 
 @pytest.mark.parametrize(

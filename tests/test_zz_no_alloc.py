@@ -2,11 +2,8 @@
 
 Its split-K partials live in the library's static per-GPU scratch array.  Two
 calls in a row -- the second smaller than the first, so it runs over what the
-first left in the scratch -- each give tq_decode's output on the same inputs:
-the same kernels and split plan, so the outputs agree to float32 rounding (the
-split kernel's wavefronts claim tiles dynamically, so the order in which a
-workgroup adds its tiles, and with it the last bits, can differ between any two
-calls).
+first left in the scratch -- each give tq_decode's output on the same inputs,
+bit for bit: the same kernels, split plan and summation order.
 """
 
 from __future__ import annotations
@@ -65,7 +62,7 @@ def test_noalloc_matches_decode_on_two_calls(hip_device):
     for cache, q, ns in ((big, q_big, 0), (small, q_small, 0), (small, q_small, 3), (big, q_big, 1)):
         ref, got = _both(hip_device, cache, q, ns)
         assert np.isfinite(ref).all()
-        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
+        np.testing.assert_array_equal(got, ref)
 
 
 def test_noalloc_rejects_oversized_plan(hip_device):
@@ -78,9 +75,9 @@ def test_noalloc_rejects_oversized_plan(hip_device):
                   0, None, None, 256, fake, None)
 
 
-def test_noalloc_deterministic_matches_decode_bit_for_bit(hip_device):
-    """With TQ_DETERMINISTIC both entry points sum the same tiles in the same order: identical bits, on two
-    calls in a row (the second smaller)."""
+def test_noalloc_matrix_kernel_matches_decode_bit_for_bit(hip_device):
+    """The matrix split kernel forced on two shapes, two calls in a row (the second smaller): both entry points
+    sum the same tiles in the same order, identical bits."""
     from torque_hip import _lib
     from torque_hip._tensors import dtype_code
 
@@ -88,7 +85,7 @@ def test_noalloc_deterministic_matches_decode_bit_for_bit(hip_device):
     small = _cache(hip_device, 2, 128, 2, 1500, seed=14)
     gen = torch.Generator(device=hip_device).manual_seed(15)
     stream = torch.cuda.current_stream(hip_device).cuda_stream
-    flags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT | _lib.TQ_DETERMINISTIC | _lib.TQ_MATRIX_PRODUCTS
+    flags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT | _lib.TQ_MATRIX_PRODUCTS
     for cache, hq, ns in ((big, 16, 6), (small, 8, 3)):
         st, cfg = cache._store, cache.config
         q = torch.randn((1, hq, cfg.head_dim), generator=gen, device=hip_device).half()
@@ -123,7 +120,7 @@ cache.append_many(key=torch.randn((1, 2, 2048, 128), generator=gen, device=dev),
 st = cache._store
 q = torch.randn((1, 8, 128), generator=gen, device=dev)
 out = torch.full((1, 8, 128), float("nan"), device=dev)
-flags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT | _lib.TQ_DETERMINISTIC
+flags = _lib.TQ_ROTATE_QUERY | _lib.TQ_INVERSE_OUTPUT
 
 
 def call():

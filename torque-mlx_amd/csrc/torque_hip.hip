@@ -231,9 +231,6 @@ struct DecodeArgs {
   const float* k_scales;
   const float* v_scales;
   int wide_iter;  // host side only: launch the kWideTokensPerIter instance
-  // decode_mx_kernel: deal every tile statically (TQ_DETERMINISTIC), so the
-  // summation order, and with it every output bit, is the same on every call
-  int static_deal;
 };
 
 // Finish one output row held by a wavefront: optional extra dense token
@@ -1662,7 +1659,6 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
   }
   a.n_splits = p.n_splits;
   a.wide_iter = p.tokens_per_iter == kWideTokensPerIter;
-  a.static_deal = (flags & TQ_DETERMINISTIC) != 0;
   a.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
   a.ws_acc = reinterpret_cast<float*>(ws + wl.acc);
   a.ws_cur_s = reinterpret_cast<float*>(ws + wl.cur_s);

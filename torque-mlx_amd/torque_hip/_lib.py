@@ -35,7 +35,6 @@ TQ_ROTATE_QUERY = 1
 TQ_INVERSE_OUTPUT = 2
 TQ_F32_PRODUCTS = 4
 TQ_MATRIX_PRODUCTS = 8
-TQ_DETERMINISTIC = 16
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int

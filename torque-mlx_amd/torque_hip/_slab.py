@@ -169,7 +169,6 @@ class SlabStore:
         inverse_output: bool,
         current: tuple[torch.Tensor, torch.Tensor] | None = None,
         n_splits: int | None = None,
-        deterministic: bool = False,
     ) -> torch.Tensor:
         """queries [L, Hq, D] -> out [L, Hq, D] float32 on the device."""
         cfg = self.config
@@ -195,7 +194,6 @@ class SlabStore:
             n_splits=n_splits,
             key_scales=self.key_scales,
             value_scales=self.value_scales,
-            deterministic=deterministic,
         )
 
     def decode_append(
@@ -209,7 +207,6 @@ class SlabStore:
         rotate_keys: bool,
         rotate_values: bool,
         n_splits: int | None = None,
-        deterministic: bool = False,
     ) -> torch.Tensor:
         """Append one token (keys/values [L, Hkv, 1, D]) and decode with it: one launch.
 
@@ -219,7 +216,7 @@ class SlabStore:
         if self.scaled:
             current = self.quantize_current(keys, values, rotate_keys=rotate_keys, rotate_values=rotate_values)
             out = self.decode(queries, rotate_query=rotate_query, inverse_output=inverse_output, current=current,
-                              n_splits=n_splits, deterministic=deterministic)
+                              n_splits=n_splits)
             self.append(keys, values, rotate_keys=rotate_keys, rotate_values=rotate_values)
             return out
         cfg = self.config
@@ -249,7 +246,6 @@ class SlabStore:
             rotate_query=rotate_query,
             inverse_output=inverse_output,
             n_splits=n_splits,
-            deterministic=deterministic,
         )
         self.length += 1
         return out

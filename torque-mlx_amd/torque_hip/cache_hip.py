@@ -54,10 +54,6 @@ class TorqueKVCacheHIP:
     rotate_values_on_append: bool = True
     rotate_queries_on_decode: bool = True
     sequence_length: int = 0
-    # Not in the reference (whose decode is always reproducible): the default matrix split kernel claims
-    # tiles dynamically, so its last output bits can differ between calls; True deals them statically
-    # (TQ_DETERMINISTIC) for bit-identical decodes.
-    deterministic_decode: bool = False
     rotation: RotationSpec = field(init=False, repr=False)
     last_decode_profile: dict[str, float] = field(init=False, repr=False)
     _store: SlabStore = field(init=False, repr=False)
@@ -194,7 +190,6 @@ class TorqueKVCacheHIP:
                     inverse_output=not self.config.fused_weights,
                     current=current,
                     n_splits=self._n_splits(),
-                    deterministic=self.deterministic_decode,
                 )
         return self._finalize_output(outputs, query_heads=query_heads, return_numpy=return_numpy)
 
@@ -237,7 +232,6 @@ class TorqueKVCacheHIP:
                     rotate_keys=self.rotate_keys_on_append,
                     rotate_values=self.rotate_values_on_append,
                     n_splits=self._n_splits(),
-                    deterministic=self.deterministic_decode,
                 )
         self.sequence_length += 1
         return self._finalize_output(outputs, query_heads=query_heads, return_numpy=return_numpy)
@@ -297,7 +291,6 @@ class TorqueKVCacheHIP:
                 rotate_query=self.rotate_queries_on_decode,
                 inverse_output=not self.config.fused_weights,
                 n_splits=self._n_splits(),
-                deterministic=self.deterministic_decode,
             )
 
     def _decode_staged(self, queries: torch.Tensor, profile: dict[str, float]) -> torch.Tensor:

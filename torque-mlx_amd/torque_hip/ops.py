@@ -117,7 +117,6 @@ def packed_decode(
     value_scales: torch.Tensor | None = None,
     f32_products: bool = False,
     matrix_products: bool = False,
-    deterministic: bool = False,
 ) -> torch.Tensor:
     """One ``tq_decode`` launch on device tensors; returns out[L, Hq, D] float32.
 
@@ -128,15 +127,12 @@ def packed_decode(
     take it (the library adds the flag), so their split plan does too.
     ``matrix_products`` (TQ_MATRIX_PRODUCTS) runs the matrix kernel wherever it
     can, also where the default plan leaves too few rows per split for it.
-    ``deterministic`` (TQ_DETERMINISTIC) makes the matrix kernel deal its tiles
-    statically, so repeated calls return identical bits.
     """
     dev = query.device
     scaled = key_scales is not None or value_scales is not None
     flags = (_lib.TQ_ROTATE_QUERY if rotate_query else 0) | (_lib.TQ_INVERSE_OUTPUT if inverse_output else 0)
     flags |= _lib.TQ_F32_PRODUCTS if f32_products or scaled else 0
     flags |= _lib.TQ_MATRIX_PRODUCTS if matrix_products else 0
-    flags |= _lib.TQ_DETERMINISTIC if deterministic else 0
     if n_splits is None or n_splits <= 0:
         n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev, bit_width=bit_width,
                                flags=flags)
@@ -202,7 +198,6 @@ def packed_decode_append(
     inverse_output: bool = False,
     n_splits: int | None = None,
     out: torch.Tensor | None = None,
-    deterministic: bool = False,
     matrix_products: bool = False,
 ) -> torch.Tensor:
     """One ``tq_decode_append`` launch: pack the new token [L, Hkv, D] into the slabs at row ``seq_len`` and
@@ -213,7 +208,6 @@ def packed_decode_append(
     dev = query.device
     append_flags = (_lib.TQ_ROTATE_KEYS if rotate_keys else 0) | (_lib.TQ_ROTATE_VALUES if rotate_values else 0)
     decode_flags = (_lib.TQ_ROTATE_QUERY if rotate_query else 0) | (_lib.TQ_INVERSE_OUTPUT if inverse_output else 0)
-    decode_flags |= _lib.TQ_DETERMINISTIC if deterministic else 0
     decode_flags |= _lib.TQ_MATRIX_PRODUCTS if matrix_products else 0
     if n_splits is None or n_splits <= 0:
         n_splits = plan_splits(num_layers, kv_heads, query_heads, head_dim, seq_len, dev, bit_width=bit_width,
