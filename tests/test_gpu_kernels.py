@@ -181,6 +181,10 @@ def test_staged_ops_match_reference(hip_device, bits):
     np.testing.assert_allclose(w, ew / ew.sum(axis=1, keepdims=True), rtol=1e-5, atol=1e-7)
     out = ops.accumulate_packed_values_batched(w, vp, cb, bit_width=bits, head_dim=128).cpu().numpy()
     np.testing.assert_allclose(out, np.einsum("bs,bsd->bd", w, cb[vi]), atol=1e-5, rtol=1e-5)
+    # the lane groups' partial sums are added in a fixed order: repeated calls agree bit for bit
+    for _ in range(3):
+        again = ops.accumulate_packed_values_batched(w, vp, cb, bit_width=bits, head_dim=128).cpu().numpy()
+        np.testing.assert_array_equal(again, out)
 
 
 @pytest.mark.parametrize("head_dim", DIMS)

@@ -1151,12 +1151,11 @@ __global__ __launch_bounds__(kBlock) void accumulate_kernel(const float* __restr
   constexpr int TPB = kWavesPerBlock * TPW;
   constexpr int ROW = Fmt::template row_bytes<D>();
   __shared__ typename Fmt::LutT s_lut[Fmt::kLutEntries];
-  __shared__ float s_acc[D];
+  __shared__ float s_part[TPB][D];  // one row per lane group: summed in a fixed order
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
   const int gi = lane / LPT, slice = lane % LPT;
   const int b = blockIdx.x;
   for (int e = tid; e < Fmt::kLutEntries; e += kBlock) s_lut[e] = Fmt::lut_entry(e, cent);
-  for (int d = tid; d < D; d += kBlock) s_acc[d] = 0.f;
   __syncthreads();
   float acc[SD];
 #pragma unroll
@@ -1170,9 +1169,13 @@ __global__ __launch_bounds__(kBlock) void accumulate_kernel(const float* __restr
     for (int i = 0; i < SD; ++i) acc[i] = fmaf(wt, x[i], acc[i]);
   }
 #pragma unroll
-  for (int i = 0; i < SD; ++i) atomicAdd(&s_acc[slice * SD + i], acc[i]);
+  for (int i = 0; i < SD; ++i) s_part[wave * TPW + gi][slice * SD + i] = acc[i];
   __syncthreads();
-  for (int d = tid; d < D; d += kBlock) out[static_cast<int64_t>(b) * D + d] = s_acc[d];
+  for (int d = tid; d < D; d += kBlock) {
+    float v = 0.f;
+    for (int r = 0; r < TPB; ++r) v += s_part[r][d];
+    out[static_cast<int64_t>(b) * D + d] = v;
+  }
 }
 
 // ============================================================== measurement
