@@ -289,16 +289,17 @@ __global__ __launch_bounds__(mx::threads_of<D>()) __attribute__((
   // mean, C4 20.55-20.60 against 20.68-20.82).  Row offsets are 32-bit (the
   // host keeps capacity * ROW < 2^31).
   const int t1 = static_cast<int>(a.seq_len);
-  const int BSTRIDE = a.n_splits * kStride;
+  const int row_splits = a.new_k != nullptr ? a.row_splits : a.n_splits;  // splits that read rows
+  const int BSTRIDE = row_splits * kStride;
   const int n_blocks = (t1 + kStride - 1) / kStride;
-  // In append mode split 0 also packs the new token, so it takes the
-  // lightest share (the blocks split n_splits - 1 would take) and splits
-  // 1.. the shares of splits 0..: the extra block of a length that does not
-  // divide evenly lands on a split without the append work (4-layer decode
-  // loop at 32768 + t tokens x 8 KV heads, 32 splits: 65.0-65.8 -> 62.2-62.4
-  // us per step).
-  const int deal = a.new_k != nullptr ? (split == 0 ? a.n_splits - 1 : split - 1) : split;
-  const int n_iter = deal < n_blocks ? (n_blocks - deal + a.n_splits - 1) / a.n_splits : 0;
+  // In append mode split 0 also packs the new token: as in decode_kernel it
+  // reads no rows where splits 1.. (row_splits of them) can take every block
+  // without a longer share, and takes the lightest share (the blocks split
+  // n_splits - 1 would take) otherwise, splits 1.. then taking the shares
+  // of splits 0.. (4-layer decode loop at 32768 + t tokens x 8 KV heads, 32
+  // splits: 65.0-65.8 -> 62.2-62.4 us per step for the lightest share).
+  const int deal = a.new_k == nullptr ? split : split > 0 ? split - 1 : row_splits < a.n_splits ? n_blocks : a.n_splits - 1;
+  const int n_iter = deal < n_blocks ? (n_blocks - deal + row_splits - 1) / row_splits : 0;
   const int n_tiles = n_iter * kTilesPerBlock;
   auto tile_row = [&](int k) {
     const unsigned uk = static_cast<unsigned>(k);

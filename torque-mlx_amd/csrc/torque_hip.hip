@@ -220,6 +220,10 @@ struct DecodeArgs {
   const float* cur_k;  // [L, Hkv, D] or null
   const float* cur_v;
   int n_splits;
+  // Splits that read rows: n_splits, or in append mode n_splits - 1 when
+  // split 0 (which also packs the new token) takes no rows and the others
+  // cover every block with no more blocks each than a deal over all splits.
+  int row_splits;
   float* ws_ml;   // [L * Hq, n_splits, 2]  (max, sum) of each split, log2 units
   float* ws_acc;  // [L * Hq, n_splits, D]  value accumulator of each split
   float* ws_cur_s; // [L * Hq]              score of the current token (log2 units)
@@ -372,18 +376,24 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
   // are 32-bit (the host keeps capacity * ROW below 2^31).  Every block but
   // the sequence's last is full.
   //
-  // In append mode split 0 also quantizes the new token, so it takes the
-  // lightest share of blocks (the one split n_splits - 1 would take) and
-  // splits 1.. take the shares of splits 0..: the extra blocks of a length
-  // that does not divide evenly then land on splits without the append
-  // work (24-layer 8K decode loop at 64 splits: 320 -> 289 us per step).
-  const int deal = (Fmt::kHasLut && a.new_k != nullptr) ? (split == 0 ? a.n_splits - 1 : split - 1) : split;
-  const int64_t t0 = static_cast<int64_t>(deal) * STRIDE;
+  // In append mode split 0 also quantizes the new token and finishes its
+  // score and value, which sets the kernel's end when it reads rows too.  So
+  // the rows go to splits 1.. only (deal index split - 1 over row_splits =
+  // n_splits - 1) where that gives no split more blocks than a deal over
+  // all of them, and split 0 deals past the last block; otherwise split 0
+  // takes the lightest share (the one split n_splits - 1 would take) and
+  // splits 1.. the shares of splits 0.. (24-layer 8K decode loop at 64
+  // splits: 320 -> 289 us per step for the lightest share, 274 -> 249 for
+  // none).
   const int t1 = static_cast<int>(a.seq_len);
-  const int BSTRIDE = a.n_splits * STRIDE;
-  const int first = static_cast<int>(t0) + wave * TPW;
   const int n_blocks = (t1 + STRIDE - 1) / STRIDE;
-  const int n_iter = deal < n_blocks ? (n_blocks - deal + a.n_splits - 1) / a.n_splits : 0;  // uniform per workgroup
+  const bool app_deal = Fmt::kHasLut && a.new_k != nullptr;
+  const int row_splits = app_deal ? a.row_splits : a.n_splits;  // splits that read rows
+  const int deal = !app_deal ? split : split > 0 ? split - 1 : row_splits < a.n_splits ? n_blocks : a.n_splits - 1;
+  const int64_t t0 = static_cast<int64_t>(deal) * STRIDE;
+  const int BSTRIDE = row_splits * STRIDE;
+  const int first = static_cast<int>(t0) + wave * TPW;
+  const int n_iter = deal < n_blocks ? (n_blocks - deal + row_splits - 1) / row_splits : 0;  // uniform per workgroup
   const uint8_t* kbase = a.k + static_cast<int64_t>(lkv) * a.cap * ROW;
   const uint8_t* vbase = a.v + static_cast<int64_t>(lkv) * a.cap * ROW;
 
@@ -831,14 +841,17 @@ __global__ __launch_bounds__(kBlock, 2) void decode_kernel(const DecodeArgs a) {
     }
   };
 
-  // The ring is unrolled NB times with no exit inside it (an iteration past
-  // n_iter reads nothing and masks every token), so the waits for each slot
-  // are the same on every trip and leave the PF prefetched slots in flight.
+  // The ring is unrolled NB times with no exit inside it, so the waits for
+  // each slot are the same on every trip and leave the PF prefetched slots in
+  // flight; loads for iterations past n_iter get an empty range and read
+  // nothing, and their compute is skipped (a wavefront-uniform branch: the
+  // longest splits of the 24-layer 8K decode loop run 3 iterations, not 4).
   for (int it = 0; it < n_iter; it += NB) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int i = it + j;
       load_iter(i + PF, kr[(j + PF) % NB], vr[(j + PF) % NB], ksr[(j + PF) % NB], vsr[(j + PF) % NB]);
+      if (j > 0 && i >= n_iter) continue;
       const bool full = first + i * BSTRIDE + (U - 1) * TPB + TPW <= t1;
       if constexpr (kMfma) {
         f32x4 c[U][SC];
@@ -1661,6 +1674,14 @@ int decode_common(int fmt, const void* query, int query_dtype, int num_layers, i
     a.rotate_new_v = (app->flags & TQ_ROTATE_VALUES) != 0;
   }
   a.n_splits = p.n_splits;
+  a.row_splits = p.n_splits;
+  if (app != nullptr && p.n_splits > 1) {
+    // split 0 packs the new token; it reads no rows when the other splits
+    // can take them all without a longer share
+    const int64_t blocks = (seq_len + p.block_rows - 1) / p.block_rows;
+    const int64_t n = p.n_splits;
+    if ((blocks + n - 2) / (n - 1) <= (blocks + n - 1) / n) a.row_splits = p.n_splits - 1;
+  }
   a.wide_iter = p.tokens_per_iter == kWideTokensPerIter;
   a.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
   a.ws_acc = reinterpret_cast<float*>(ws + wl.acc);
