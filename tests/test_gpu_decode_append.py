@@ -113,9 +113,10 @@ def test_mixed_kv_dtypes_quantize_at_float32(hip_device):
 @pytest.mark.parametrize("bits,head_dim", [(4, 128), (4, 256), (2, 128)])
 def test_decode_append_against_oracle_and_split_counts(hip_device, bits, head_dim):
     """3000 rows: 1 and 3 splits run the matrix kernel (24 and 8 blocks of 128 rows per split), 64 splits the
-    float32 kernel; 5 and 7 splits force the matrix kernel onto uneven shares (24 blocks: 5/5/5/5/4 and
-    4/4/4/3/3/3/3), where the appending split 0 takes the lightest one.  Every output matches the oracle's
-    append-then-decode."""
+    float32 kernel; 5 and 7 splits force the matrix kernel onto uneven shares of the 24 blocks.  The appending
+    split 0 takes the lightest share at 3 and 5 splits (splits 1.. alone would need 12 and 6 blocks each) and
+    no rows at 7 and 64 (the other splits take 4 blocks each of 128 rows, or 2-3 of the float32 kernel's,
+    as a deal over all the splits would).  Every output matches the oracle's append-then-decode."""
     import torque_hip as th
     from torque_hip import _lib
     from torque_hip.ops import packed_decode_append
